@@ -1,0 +1,151 @@
+/* pk_hip.h - the C ABI of libpkhip.so, libpktito's int8 product path on one
+ * MI355X (gfx950).
+ *
+ * libpktito's backend seam is a table of function pointers (the reference's
+ * backend/kernels.h:242-278, pk_kernels). The int8 path is two of them:
+ *
+ *   quantize   fp32 activations to int8, per column in blocks of qb, a scale
+ *              a block                     (backend/kernels.h:47-58)
+ *   gemm_q8    the int8 product with exact int32 sums and the fixed fp32
+ *              epilogue                    (backend/kernels.h:60-78)
+ *
+ * This library computes both on the GPU with the reference's bits: the int8
+ * activations, their scales and every fp32 output are those of the
+ * reference's scalar ref backend (backend/ref/kernels.c:24-86) on the same
+ * inputs. The entry points come in three groups:
+ *
+ *   1. the drop-in: pk_hip_quantize and pk_hip_gemm_q8 take host pointers and
+ *      the arguments of the table's quantize and gemm_q8, and return with the
+ *      results in host memory, as the table's functions do;
+ *   2. the upload: the model-load step that repacks each PK_Q8 matrix once
+ *      into HBM (the reference binds matrices at core/model.c:345-363);
+ *   3. the device-resident path: the same two operations on device pointers,
+ *      asynchronous on a caller's stream, for callers that keep activations
+ *      in HBM.
+ *
+ * Every function returns PK_HIP_OK or an error code (pk_hip_strerror names it,
+ * pk_hip_last_error gives the calling thread's last message); nothing falls
+ * back to the CPU. No function here prints.
+ */
+#ifndef PK_HIP_H
+#define PK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The activations of one product: the reference's pk_act
+ * (backend/kernels.h:41-45), field for field, so a pk_act * may be passed
+ * wherever a pk_hip_act * is taken.
+ *   q  [T][n] int8, column t at q + t * n
+ *   d  [T][n / qb] fp32, each block's scale */
+typedef struct {
+    int8_t   *q;
+    float    *d;
+    uint32_t  n, qb, T;
+} pk_hip_act;
+
+enum {
+    PK_HIP_OK = 0,
+    PK_HIP_EINVAL = 1,      /* arguments outside the contract */
+    PK_HIP_ENODEV = 2,      /* no usable gfx950 device */
+    PK_HIP_ENOMEM = 3,      /* a device or pinned allocation failed */
+    PK_HIP_EDEVICE = 4,     /* a HIP call or a kernel launch failed */
+    PK_HIP_ENOTUP = 5,      /* gemm_q8's w is inside no uploaded matrix */
+    PK_HIP_EROUND = 6,      /* the caller's rounding mode is one this entry does not take */
+};
+
+/* The error code's name, and the calling thread's last error message. */
+const char *pk_hip_strerror(int err);
+const char *pk_hip_last_error(void);
+
+/* Opens the device (the one current on the calling thread, else device 0)
+ * once a process; later calls return the first call's result. Every other
+ * function calls it. The environment's PKTITO_HIP_DISABLE=1 makes it fail
+ * with PK_HIP_ENODEV, so a caller's no-device path can be tested anywhere. */
+int pk_hip_init(void);
+
+/* ------------------------------------------------------------ upload --- */
+
+/* Repacks the PK_Q8 matrix q (rows x cols, the reference's core/pkf.h:28-41
+ * layout) into HBM with its rows scales s, once, and records the host range
+ * [q, q + rows * cols) so that gemm_q8 calls whose w points at any whole
+ * panel inside it run on the device copy. rows % 16 == 0, cols % 32 == 0,
+ * cols <= 16384 (core/model.c:354). Replaces nothing in the reference: it is
+ * the step a GPU backend adds after core/model.c's load_file (:783-811). The
+ * host bytes must not change while the matrix is uploaded. */
+int pk_hip_upload_q8(const int8_t *q, const float *s, uint32_t rows, uint32_t cols);
+
+/* Frees the device copy of the matrix whose host bytes start at q
+ * (core/model.c:868-883's pk_model_free gains this call); all of them. */
+int pk_hip_release_q8(const int8_t *q);
+void pk_hip_release_all(void);
+
+/* -------------------------------------------------------- the drop-in --- */
+
+/* The table's quantize (backend/kernels.h:47-58, :256), on host pointers:
+ * a->q, a->d and x are host memory; returns with q and d written.
+ * Round-to-nearest only (PK_HIP_EROUND otherwise). */
+int pk_hip_quantize(pk_hip_act *a, const float *x, size_t xs);
+
+/* The table's gemm_q8 (backend/kernels.h:60-78, :257-258), on host pointers:
+ * out[t * os + r] for r < rows, t < a->T, with w pointing at a whole panel of
+ * an uploaded matrix and ws, bias its scales and bias from that panel on.
+ * The floats between one column's outputs and the next are not touched.
+ * Any of the four IEEE rounding modes the calling thread has set. */
+int pk_hip_gemm_q8(float *out, size_t os, const int8_t *w, const float *ws, const float *bias,
+                   uint32_t rows, const pk_hip_act *a, int add);
+
+/* ------------------------------------------- the device-resident path --- */
+
+/* An uploaded matrix, found by its host bytes; NULL if none holds q. */
+typedef struct pk_hip_q8 pk_hip_q8;
+const pk_hip_q8 *pk_hip_q8_find(const int8_t *q);
+/* Its device scales (rows floats), rows and cols. */
+const float *pk_hip_q8_scales(const pk_hip_q8 *m);
+uint32_t pk_hip_q8_rows(const pk_hip_q8 *m);
+uint32_t pk_hip_q8_cols(const pk_hip_q8 *m);
+
+/* quantize on device pointers (a->q, a->d, x), enqueued on stream (a
+ * hipStream_t; NULL for the null stream). q and x 16-byte aligned, xs a
+ * multiple of 4 floats. Round-to-nearest. */
+int pk_hip_quantize_dev(pk_hip_act *a, const float *x, size_t xs, void *stream);
+
+/* gemm_q8 on device pointers: out, ws, bias, a->q and a->d in device memory;
+ * the weights are rows [r0, r0 + rows) of the uploaded matrix m (r0 and rows
+ * multiples of 16). ws and bias point at row r0's scale and bias (ws may be
+ * pk_hip_q8_scales(m) + r0). a->q 16-byte aligned. rmode is the IEEE
+ * rounding of the epilogue: 0 to nearest, 1 upward, 2 downward, 3 toward
+ * zero. Enqueued on stream; returns once launched. */
+int pk_hip_gemm_q8_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
+                       const float *ws, const float *bias, const pk_hip_act *a, int add,
+                       int rmode, void *stream);
+
+/* One segment of a grouped product: its own activations and outputs. */
+typedef struct {
+    float      *out;
+    size_t      os;
+    pk_hip_act  a;
+} pk_hip_seg;
+
+/* gemm_q8 of one matrix over nseg segments of activations in a single launch
+ * (the ragged batch of segments of different lengths that the reference runs
+ * as concurrent lanes, core/asr.c:346-570): each segment's outputs are the
+ * bits pk_hip_gemm_q8_dev gives it alone. Device pointers throughout; the
+ * segments share n and qb; nseg <= 64. */
+int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, const float *ws,
+                               const float *bias, const pk_hip_seg *segs, uint32_t nseg, int add,
+                               void *stream);
+
+/* Statistics of the last device product launched on this thread: the kernel
+ * variant's name, for profiling and tests. */
+const char *pk_hip_last_kernel(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PK_HIP_H */

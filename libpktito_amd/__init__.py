@@ -1,0 +1,218 @@
+"""libpktito's int8 product path on one MI355X: the Python side of the C ABI.
+
+The reference's seam is a C table, ``pk_kernels`` (backend/kernels.h:242-278
+in peterheb/libpktito), whose int8 entries are
+
+    quantize(pk_act *a, const float *x, size_t xs)
+    gemm_q8(float *out, size_t os, const int8_t *w, const float *ws,
+            const float *bias, uint32_t rows, const pk_act *a, int add)
+
+``libpkhip.so`` (include/pk_hip.h) computes both on the GPU with the
+reference's bits. This module binds it with ctypes and mirrors the two
+functions with the same names, argument meanings and edge behaviour, on numpy
+arrays (the host-pointer drop-in) or on device tensors (the device-resident
+path; torch is used only for device memory and streams). There is no CPU
+path here: if libpkhip.so is missing or no gfx950 device answers, calls raise.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libpkhip.so")
+
+PK_HIP_OK = 0
+PK_HIP_EINVAL = 1
+PK_HIP_ENODEV = 2
+PK_HIP_ENOMEM = 3
+PK_HIP_EDEVICE = 4
+PK_HIP_ENOTUP = 5
+PK_HIP_EROUND = 6
+
+
+class PkHipError(RuntimeError):
+    """A pk_hip_* call returned an error code."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"pk_hip error {code}: {msg}")
+        self.code = code
+
+
+class Act(ctypes.Structure):
+    """pk_act (backend/kernels.h:41-45): q [T][n] int8, d [T][n/qb] fp32."""
+    _fields_ = [("q", ctypes.c_void_p), ("d", ctypes.c_void_p),
+                ("n", ctypes.c_uint32), ("qb", ctypes.c_uint32), ("T", ctypes.c_uint32)]
+
+
+class Seg(ctypes.Structure):
+    """pk_hip_seg: one segment of a grouped product."""
+    _fields_ = [("out", ctypes.c_void_p), ("os", ctypes.c_size_t), ("a", Act)]
+
+
+_lib = None
+
+# every function include/pk_hip.h declares, with its ctypes signature
+_SIGS = {
+    "pk_hip_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+    "pk_hip_last_error": (ctypes.c_char_p, []),
+    "pk_hip_last_kernel": (ctypes.c_char_p, []),
+    "pk_hip_init": (ctypes.c_int, []),
+    "pk_hip_upload_q8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32]),
+    "pk_hip_release_q8": (ctypes.c_int, [ctypes.c_void_p]),
+    "pk_hip_release_all": (None, []),
+    "pk_hip_quantize": (ctypes.c_int, [ctypes.POINTER(Act), ctypes.c_void_p, ctypes.c_size_t]),
+    "pk_hip_gemm_q8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(Act), ctypes.c_int]),
+    "pk_hip_q8_find": (ctypes.c_void_p, [ctypes.c_void_p]),
+    "pk_hip_q8_scales": (ctypes.c_void_p, [ctypes.c_void_p]),
+    "pk_hip_q8_rows": (ctypes.c_uint32, [ctypes.c_void_p]),
+    "pk_hip_q8_cols": (ctypes.c_uint32, [ctypes.c_void_p]),
+    "pk_hip_quantize_dev": (ctypes.c_int, [ctypes.POINTER(Act), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "pk_hip_gemm_q8_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_uint32,
+                                          ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(Act),
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "pk_hip_gemm_q8_grouped_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(Seg),
+                                                  ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]),
+}
+
+
+def lib():
+    """The loaded libpkhip.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run python -m libpktito_amd.build "
+                               "(the int8 path has no CPU fallback)")
+        # One HIP runtime a process: torch's wheel carries its own
+        # libamdhip64.so.7. Loaded first, it is the one libpkhip.so binds to
+        # (same soname); loaded after libpkhip.so had pulled in /opt/rocm's,
+        # torch would start a second runtime that sees no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _check(code):
+    if code != PK_HIP_OK:
+        raise PkHipError(code, lib().pk_hip_last_error().decode(errors="replace"))
+
+
+def init():
+    """Open the device (pk_hip_init); raises PkHipError when none is usable."""
+    _check(lib().pk_hip_init())
+
+
+def last_kernel():
+    """The kernel variant the calling thread launched last."""
+    return lib().pk_hip_last_kernel().decode()
+
+
+def _ptr(a):
+    return a.ctypes.data if a is not None else None
+
+
+# ------------------------------------------------------------ the drop-in ---
+
+def make_act(q, d, n, qb, T):
+    """A pk_act over numpy arrays (or raw addresses)."""
+    qp = q if isinstance(q, int) else _ptr(q)
+    dp = d if isinstance(d, int) else _ptr(d)
+    return Act(qp, dp, n, qb, T)
+
+
+def quantize(a, x, xs):
+    """pk_k_quantize (backend/kernels.h:47-58) on host arrays: x holds T
+    columns of a.n floats, column t at x[t * xs:]; fills a.q and a.d."""
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    _check(lib().pk_hip_quantize(ctypes.byref(a), _ptr(x), xs))
+
+
+def gemm_q8(out, os_, w, ws, bias, rows, a, add, w_offset=0, out_offset=0):
+    """pk_k_gemm_q8 (backend/kernels.h:60-78) on host arrays. w is the whole
+    uploaded PK_Q8 matrix's bytes and w_offset the byte offset of the call's
+    first panel inside it (the reference's w + r0 * cols); ws and bias start
+    at that panel's first row; out_offset is the float offset of the call's
+    first output (out + r0)."""
+    assert out.dtype == np.float32 and ws.dtype == np.float32
+    wp = _ptr(w) + w_offset
+    op = _ptr(out) + 4 * out_offset
+    _check(lib().pk_hip_gemm_q8(op, os_, wp, _ptr(ws), _ptr(bias), rows, ctypes.byref(a), int(add)))
+
+
+class Q8Matrix:
+    """A PK_Q8 matrix uploaded to HBM, repacked once (the model-load step).
+    Keeps its host arrays alive, since the registry is keyed on their address."""
+
+    def __init__(self, q, s):
+        assert q.dtype == np.int8 and s.dtype == np.float32
+        rows = s.shape[0]
+        cols = q.size // rows
+        self.q, self.s, self.rows, self.cols = q, s, rows, cols
+        _check(lib().pk_hip_upload_q8(_ptr(q), _ptr(s), rows, cols))
+        self.handle = lib().pk_hip_q8_find(_ptr(q))
+
+    @property
+    def dev_scales(self):
+        return lib().pk_hip_q8_scales(self.handle)
+
+    def release(self):
+        if self.handle:
+            _check(lib().pk_hip_release_q8(_ptr(self.q)))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.release()
+
+
+# ------------------------------------------------ the device-resident path ---
+
+def _dptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return stream
+
+
+def quantize_dev(q, d, x, n, qb, T, xs, stream=None):
+    """quantize on device tensors: x float32 (T rows at stride xs), q int8
+    [T, n], d float32 [T, n / qb]."""
+    a = Act(_dptr(q), _dptr(d), n, qb, T)
+    _check(lib().pk_hip_quantize_dev(ctypes.byref(a), _dptr(x), xs, _stream(stream)))
+
+
+def gemm_q8_dev(out, os_, m, r0, rows, ws, bias, q, d, n, qb, T, add, rmode=0, stream=None,
+                ws_ptr=None, out_ptr=None):
+    """gemm_q8 on device tensors against an uploaded Q8Matrix m, rows
+    [r0, r0 + rows). ws (or ws_ptr) and bias start at row r0; out (or
+    out_ptr) at the first output."""
+    a = Act(_dptr(q), _dptr(d), n, qb, T)
+    wsp = ws_ptr if ws_ptr is not None else _dptr(ws)
+    op = out_ptr if out_ptr is not None else _dptr(out)
+    _check(lib().pk_hip_gemm_q8_dev(op, os_, m.handle, r0, rows, wsp, _dptr(bias),
+                                    ctypes.byref(a), int(add), rmode, _stream(stream)))
+
+
+def gemm_q8_grouped_dev(m, r0, rows, ws_ptr, bias, segs, add, stream=None):
+    """One launch over segments [(out, os, q, d, n, qb, T), ...] of device tensors."""
+    arr = (Seg * len(segs))()
+    for i, (out, os_, q, d, n, qb, T) in enumerate(segs):
+        arr[i] = Seg(_dptr(out), os_, Act(_dptr(q), _dptr(d), n, qb, T))
+    _check(lib().pk_hip_gemm_q8_grouped_dev(m.handle, r0, rows, ws_ptr, _dptr(bias), arr, len(segs),
+                                            int(add), _stream(stream)))

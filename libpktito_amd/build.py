@@ -1,0 +1,49 @@
+"""Builds libpkhip.so, the C-ABI library of the int8 product path, in-tree.
+
+    python -m libpktito_amd.build        (or libpktito_amd.build.build())
+
+One hipcc line for gfx950: the kernels (csrc/q8_kernels.hip) and the runtime
+(csrc/pk_hip.cpp). The flags are part of the path's contract:
+  -ffp-contract=off    no multiply and add the code writes apart is fused: the
+                       epilogue's operations are the reference's, one rounding
+                       each (its Makefile builds with the same flag);
+  no -ffast-math, no -fgpu-flush-denormals-to-zero: a block's scale can be
+                       subnormal, and the division must stay IEEE;
+  -Xclang -target-feature -Xclang -packed-fp32-ops  (disabled: see below)
+The packed-fp32 feature is switched off so the compiler makes no v_pk_*_f32
+from the epilogue's float code.
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB = os.path.join(HERE, "libpkhip.so")
+SOURCES = [os.path.join(HERE, "csrc", "q8_kernels.hip"), os.path.join(HERE, "csrc", "pk_hip.cpp")]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-result",
+]
+
+
+def build(verbose=False):
+    """Compile libpkhip.so; raises CalledProcessError with hipcc's output on failure."""
+    cmd = [HIPCC] + FLAGS + ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc")]
+    cmd += SOURCES + ["-o", LIB + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise subprocess.CalledProcessError(r.returncode, cmd, output=out)
+    if verbose and out.strip():
+        print(out)
+    os.replace(LIB + ".tmp", LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,544 @@
+/* The runtime behind include/pk_hip.h: device set-up, the upload registry,
+ * per-call staging for the host-pointer drop-in, and argument checking for
+ * every entry. The kernels are in q8_kernels.hip.
+ *
+ * The reference's seam (backend/kernels.h:242-278) is synchronous, takes host
+ * pointers and is called concurrently from a pool's threads on disjoint
+ * output tiles (core/passes.c:60-72). So each host-pointer call takes a
+ * context of its own from a pool - a stream and its device staging - for the
+ * length of the call, and returns with the results in host memory. Contexts
+ * are made on demand and kept for the process, so concurrent calls never
+ * share one and no call waits for another's.
+ */
+#include "pk_hip.h"
+#include "q8_internal.h"
+
+#include <cfenv>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <shared_mutex>
+#include <vector>
+
+struct pk_hip_q8 {
+    const int8_t *hq;           /* host PK_Q8 bytes, the registry's key */
+    const float *hs;
+    uint32_t rows, cols, ku;
+    int8_t *w;                  /* device units */
+    float *s;                   /* device scales */
+};
+
+namespace {
+
+thread_local char g_err[256];
+thread_local const char *g_kernel = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(PK_HIP_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define PK_TRY(call)                                          \
+    do {                                                      \
+        hipError_t e_ = (call);                               \
+        if (e_ != hipSuccess) return hip_fail(e_, #call);     \
+    } while (0)
+
+std::once_flag g_once;
+int g_init = PK_HIP_ENODEV;
+int g_dev = -1;
+char g_init_err[256];
+
+void init_once() {
+    const char *off = getenv("PKTITO_HIP_DISABLE");
+    if (off && *off && strcmp(off, "0")) {
+        snprintf(g_init_err, sizeof g_init_err, "PKTITO_HIP_DISABLE is set");
+        g_init = PK_HIP_ENODEV;
+        return;
+    }
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count < 1) {
+        snprintf(g_init_err, sizeof g_init_err, "no HIP device");
+        g_init = PK_HIP_ENODEV;
+        return;
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        dev = 0;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) {
+        snprintf(g_init_err, sizeof g_init_err, "hipGetDeviceProperties failed");
+        g_init = PK_HIP_ENODEV;
+        return;
+    }
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+        snprintf(g_init_err, sizeof g_init_err, "device %d is %s, not gfx950", dev, p.gcnArchName);
+        g_init = PK_HIP_ENODEV;
+        return;
+    }
+    g_dev = dev;
+    g_init = PK_HIP_OK;
+}
+
+/* ---------------------------------------------------------- registry --- */
+
+std::shared_mutex g_reg_mu;
+std::map<uintptr_t, pk_hip_q8 *> g_reg;     /* host start -> matrix */
+
+/* the matrix whose host bytes hold p, or NULL; caller holds g_reg_mu */
+pk_hip_q8 *holding(const void *p) {
+    const uintptr_t a = (uintptr_t)p;
+    auto it = g_reg.upper_bound(a);
+    if (it == g_reg.begin())
+        return nullptr;
+    --it;
+    pk_hip_q8 *m = it->second;
+    return a < it->first + (uintptr_t)m->rows * m->cols ? m : nullptr;
+}
+
+void free_matrix(pk_hip_q8 *m) {
+    (void)hipSetDevice(g_dev);
+    (void)hipFree(m->w);
+    (void)hipFree(m->s);
+    delete m;
+}
+
+/* ----------------------------------------------------------- contexts --- */
+
+struct Ctx {
+    hipStream_t stream = nullptr;
+    char *dev = nullptr;
+    size_t cap = 0;
+};
+
+std::mutex g_ctx_mu;
+std::vector<Ctx *> g_idle;
+
+struct Lease {
+    Ctx *c = nullptr;
+    ~Lease() {
+        if (c) {
+            std::lock_guard<std::mutex> lk(g_ctx_mu);
+            g_idle.push_back(c);
+        }
+    }
+};
+
+int lease(Lease &l) {
+    {
+        std::lock_guard<std::mutex> lk(g_ctx_mu);
+        if (!g_idle.empty()) {
+            l.c = g_idle.back();
+            g_idle.pop_back();
+        }
+    }
+    PK_TRY(hipSetDevice(g_dev));
+    if (!l.c) {
+        Ctx *c = new Ctx;
+        hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            delete c;
+            return hip_fail(e, "hipStreamCreateWithFlags");
+        }
+        l.c = c;
+    }
+    return PK_HIP_OK;
+}
+
+int reserve(Ctx *c, size_t bytes) {
+    if (bytes <= c->cap)
+        return PK_HIP_OK;
+    if (c->dev) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(c->dev);
+        c->dev = nullptr;
+        c->cap = 0;
+    }
+    size_t want = bytes + bytes / 4 + (1 << 20);
+    if (hipMalloc(&c->dev, want) != hipSuccess) {
+        c->dev = nullptr;
+        return fail(PK_HIP_ENOMEM, "hipMalloc of %zu bytes of staging failed", want);
+    }
+    c->cap = want;
+    return PK_HIP_OK;
+}
+
+size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int rmode_of_host() {
+    switch (fegetround()) {
+    case FE_TONEAREST: return 0;
+    case FE_UPWARD: return 1;
+    case FE_DOWNWARD: return 2;
+    case FE_TOWARDZERO: return 3;
+    default: return -1;
+    }
+}
+
+/* The contract of backend/kernels.h:47-58 and :60-83 for an act. */
+int check_act(const pk_hip_act *a, bool for_gemm) {
+    if (!a)
+        return fail(PK_HIP_EINVAL, "act is NULL");
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!a->q || !a->d)
+        return fail(PK_HIP_EINVAL, "act q or d is NULL");
+    if (a->n == 0 || a->qb == 0 || a->n % a->qb)
+        return fail(PK_HIP_EINVAL, "qb %u does not divide n %u", a->qb, a->n);
+    if (a->n % 16 || a->qb % 16)
+        return fail(PK_HIP_EINVAL, "n %u and qb %u must be multiples of 16", a->n, a->qb);
+    if (for_gemm) {
+        if (a->n % 32)
+            return fail(PK_HIP_EINVAL, "gemm_q8 takes n a multiple of 32, not %u", a->n);
+        if (a->qb != a->n && a->qb % 32)
+            return fail(PK_HIP_EINVAL, "gemm_q8 takes blocks of a multiple of 32, not %u", a->qb);
+        if (a->n > 16384)
+            return fail(PK_HIP_EINVAL, "n %u is over 16384", a->n);
+    }
+    return PK_HIP_OK;
+}
+
+int launch_quant(pk_hip_act *a, const float *x, size_t xs, hipStream_t s) {
+    const char *name = "";
+    if (pkq8::launch_quantize(a->q, a->d, x, xs, a->n, a->qb, a->T, s, &name))
+        return hip_fail(hipGetLastError(), "quantize launch");
+    g_kernel = name;
+    return PK_HIP_OK;
+}
+
+int launch_product(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
+                   const float *ws, const float *bias, const pk_hip_act *a, int add, int rmode,
+                   hipStream_t s) {
+    pkq8::GemmArgs g;
+    g.w = m->w + (size_t)(r0 / 16) * m->ku * pkq8::kUnitBytes;
+    g.ws = ws;
+    g.bias = bias;
+    g.rows = rows;
+    g.n = a->n;
+    g.ku = m->ku;
+    g.qb = a->qb;
+    g.nb = a->n / a->qb;
+    g.add = add;
+    g.rmode = rmode;
+    pkq8::SegTable tab;
+    tab.nseg = 1;
+    tab.s[0] = pkq8::Seg{ out, a->q, a->d, (uint64_t)os, a->T, 0 };
+    const char *name = "";
+    if (pkq8::launch_gemm(g, tab, s, &name))
+        return hip_fail(hipGetLastError(), "gemm_q8 launch");
+    g_kernel = name;
+    return PK_HIP_OK;
+}
+
+int check_panel(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, uint32_t n) {
+    if (rows % 16 || r0 % 16)
+        return fail(PK_HIP_EINVAL, "rows %u and r0 %u must be multiples of 16", rows, r0);
+    if ((uint64_t)r0 + rows > m->rows)
+        return fail(PK_HIP_EINVAL, "rows [%u, %u) are outside the matrix's %u", r0, r0 + rows, m->rows);
+    if (n != m->cols)
+        return fail(PK_HIP_EINVAL, "act n %u is not the matrix's %u inputs", n, m->cols);
+    return PK_HIP_OK;
+}
+
+}  // namespace
+
+/* ================================================================ ABI === */
+
+extern "C" {
+
+const char *pk_hip_strerror(int err) {
+    switch (err) {
+    case PK_HIP_OK: return "ok";
+    case PK_HIP_EINVAL: return "invalid argument";
+    case PK_HIP_ENODEV: return "no usable gfx950 device";
+    case PK_HIP_ENOMEM: return "out of device memory";
+    case PK_HIP_EDEVICE: return "HIP error";
+    case PK_HIP_ENOTUP: return "matrix not uploaded";
+    case PK_HIP_EROUND: return "unsupported rounding mode";
+    default: return "unknown error";
+    }
+}
+
+const char *pk_hip_last_error(void) { return g_err; }
+
+const char *pk_hip_last_kernel(void) { return g_kernel; }
+
+int pk_hip_init(void) {
+    std::call_once(g_once, init_once);
+    if (g_init != PK_HIP_OK)
+        return fail(g_init, "%s", g_init_err);
+    return PK_HIP_OK;
+}
+
+int pk_hip_upload_q8(const int8_t *q, const float *s, uint32_t rows, uint32_t cols) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!q || !s)
+        return fail(PK_HIP_EINVAL, "upload: q or s is NULL");
+    if (rows == 0 || rows % 16 || cols == 0 || cols % 32 || cols > 16384)
+        return fail(PK_HIP_EINVAL, "upload: a q8 matrix is 16 rows by 32 inputs at a time, at most "
+                                   "16384 inputs; not %u x %u", rows, cols);
+    {
+        std::shared_lock<std::shared_mutex> lk(g_reg_mu);
+        if (holding(q) || holding(q + (size_t)rows * cols - 1))
+            return fail(PK_HIP_EINVAL, "upload: host bytes at %p overlap an uploaded matrix", (const void *)q);
+    }
+    PK_TRY(hipSetDevice(g_dev));
+    pk_hip_q8 *m = new pk_hip_q8{ q, s, rows, cols, pkq8::units_per_panel(cols), nullptr, nullptr };
+    const size_t raw = (size_t)rows * cols;
+    const size_t packed = (size_t)(rows / 16) * m->ku * pkq8::kUnitBytes;
+    int8_t *tmp = nullptr;
+    hipError_t he = hipMalloc(&tmp, raw);
+    if (he == hipSuccess) he = hipMalloc(&m->w, packed);
+    if (he == hipSuccess) he = hipMalloc(&m->s, rows * sizeof(float));
+    if (he != hipSuccess) {
+        (void)hipFree(tmp);
+        (void)hipFree(m->w);
+        (void)hipFree(m->s);
+        delete m;
+        return fail(PK_HIP_ENOMEM, "upload: hipMalloc failed for a %u x %u matrix", rows, cols);
+    }
+    he = hipMemcpy(tmp, q, raw, hipMemcpyHostToDevice);
+    if (he == hipSuccess) he = hipMemcpy(m->s, s, rows * sizeof(float), hipMemcpyHostToDevice);
+    if (he == hipSuccess && pkq8::launch_repack(m->w, tmp, rows, cols, nullptr)) he = hipGetLastError();
+    if (he == hipSuccess) he = hipDeviceSynchronize();
+    (void)hipFree(tmp);
+    if (he != hipSuccess) {
+        free_matrix(m);
+        return hip_fail(he, "upload");
+    }
+    std::unique_lock<std::shared_mutex> lk(g_reg_mu);
+    g_reg[(uintptr_t)q] = m;
+    return PK_HIP_OK;
+}
+
+int pk_hip_release_q8(const int8_t *q) {
+    pk_hip_q8 *m = nullptr;
+    {
+        std::unique_lock<std::shared_mutex> lk(g_reg_mu);
+        auto it = g_reg.find((uintptr_t)q);
+        if (it == g_reg.end())
+            return fail(PK_HIP_EINVAL, "release: no matrix starts at %p", (const void *)q);
+        m = it->second;
+        g_reg.erase(it);
+    }
+    free_matrix(m);
+    return PK_HIP_OK;
+}
+
+void pk_hip_release_all(void) {
+    std::unique_lock<std::shared_mutex> lk(g_reg_mu);
+    for (auto &kv : g_reg)
+        free_matrix(kv.second);
+    g_reg.clear();
+}
+
+const pk_hip_q8 *pk_hip_q8_find(const int8_t *q) {
+    std::shared_lock<std::shared_mutex> lk(g_reg_mu);
+    return holding(q);
+}
+
+const float *pk_hip_q8_scales(const pk_hip_q8 *m) { return m ? m->s : nullptr; }
+uint32_t pk_hip_q8_rows(const pk_hip_q8 *m) { return m ? m->rows : 0; }
+uint32_t pk_hip_q8_cols(const pk_hip_q8 *m) { return m ? m->cols : 0; }
+
+int pk_hip_quantize(pk_hip_act *a, const float *x, size_t xs) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if ((e = check_act(a, false)))
+        return e;
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!x || xs < a->n)
+        return fail(PK_HIP_EINVAL, "quantize: x is NULL or its stride %zu is under n %u", xs, a->n);
+    if (rmode_of_host() != 0)
+        return fail(PK_HIP_EROUND, "quantize runs to nearest only");
+    Lease l;
+    if ((e = lease(l)))
+        return e;
+    const size_t n = a->n, T = a->T, nb = n / a->qb;
+    const size_t xb = up256(T * n * sizeof(float)), qbytes = up256(T * n);
+    if ((e = reserve(l.c, xb + qbytes + up256(T * nb * sizeof(float)))))
+        return e;
+    float *dx = (float *)l.c->dev;
+    int8_t *dq = (int8_t *)(l.c->dev + xb);
+    float *dd = (float *)(l.c->dev + xb + qbytes);
+    hipStream_t s = l.c->stream;
+    PK_TRY(hipMemcpy2DAsync(dx, n * sizeof(float), x, xs * sizeof(float), n * sizeof(float), T,
+                            hipMemcpyHostToDevice, s));
+    pk_hip_act da = { dq, dd, a->n, a->qb, a->T };
+    if ((e = launch_quant(&da, dx, n, s)))
+        return e;
+    PK_TRY(hipMemcpyAsync(a->q, dq, T * n, hipMemcpyDeviceToHost, s));
+    PK_TRY(hipMemcpyAsync(a->d, dd, T * nb * sizeof(float), hipMemcpyDeviceToHost, s));
+    PK_TRY(hipStreamSynchronize(s));
+    return PK_HIP_OK;
+}
+
+int pk_hip_gemm_q8(float *out, size_t os, const int8_t *w, const float *ws, const float *bias,
+                   uint32_t rows, const pk_hip_act *a, int add) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if ((e = check_act(a, true)))
+        return e;
+    if (a->T == 0)
+        return PK_HIP_OK;          /* no columns: nothing read, nothing written */
+    if (!out || !w || !ws)
+        return fail(PK_HIP_EINVAL, "gemm_q8: out, w or ws is NULL");
+    if (a->T > 1 && os < rows)
+        return fail(PK_HIP_EINVAL, "gemm_q8: output stride %zu is under rows %u", os, rows);
+    const int rmode = rmode_of_host();
+    if (rmode < 0)
+        return fail(PK_HIP_EROUND, "gemm_q8: unknown rounding mode");
+    const pk_hip_q8 *m;
+    uint32_t r0;
+    {
+        std::shared_lock<std::shared_mutex> lk(g_reg_mu);
+        m = holding(w);
+        if (!m)
+            return fail(PK_HIP_ENOTUP, "gemm_q8: w %p is inside no uploaded matrix", (const void *)w);
+        const size_t off = (size_t)(w - m->hq), panel = (size_t)16 * m->cols;
+        if (off % panel)
+            return fail(PK_HIP_EINVAL, "gemm_q8: w is not at a panel of its matrix");
+        r0 = (uint32_t)(off / panel) * 16;
+    }
+    if ((e = check_panel(m, r0, rows, a->n)))
+        return e;
+    Lease l;
+    if ((e = lease(l)))
+        return e;
+    const size_t n = a->n, T = a->T, nb = n / a->qb, R = rows;
+    const size_t bq = up256(T * n), bd = up256(T * nb * 4), bw = up256(R * 4), bo = up256(T * R * 4);
+    if ((e = reserve(l.c, bq + bd + 2 * bw + bo)))
+        return e;
+    char *p = l.c->dev;
+    int8_t *dq = (int8_t *)p;
+    float *dd = (float *)(p + bq);
+    float *dws = (float *)(p + bq + bd);
+    float *db = (float *)(p + bq + bd + bw);
+    float *dout = (float *)(p + bq + bd + 2 * bw);
+    hipStream_t s = l.c->stream;
+    PK_TRY(hipMemcpyAsync(dq, a->q, T * n, hipMemcpyHostToDevice, s));
+    PK_TRY(hipMemcpyAsync(dd, a->d, T * nb * 4, hipMemcpyHostToDevice, s));
+    PK_TRY(hipMemcpyAsync(dws, ws, R * 4, hipMemcpyHostToDevice, s));
+    if (bias)
+        PK_TRY(hipMemcpyAsync(db, bias, R * 4, hipMemcpyHostToDevice, s));
+    if (add) {
+        if (T == 1)
+            PK_TRY(hipMemcpyAsync(dout, out, R * 4, hipMemcpyHostToDevice, s));
+        else
+            PK_TRY(hipMemcpy2DAsync(dout, R * 4, out, os * 4, R * 4, T, hipMemcpyHostToDevice, s));
+    }
+    pk_hip_act da = { dq, dd, a->n, a->qb, a->T };
+    if ((e = launch_product(dout, R, m, r0, rows, dws, bias ? db : nullptr, &da, add, rmode, s)))
+        return e;
+    if (T == 1)
+        PK_TRY(hipMemcpyAsync(out, dout, R * 4, hipMemcpyDeviceToHost, s));
+    else
+        PK_TRY(hipMemcpy2DAsync(out, os * 4, dout, R * 4, R * 4, T, hipMemcpyDeviceToHost, s));
+    PK_TRY(hipStreamSynchronize(s));
+    return PK_HIP_OK;
+}
+
+int pk_hip_quantize_dev(pk_hip_act *a, const float *x, size_t xs, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if ((e = check_act(a, false)))
+        return e;
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!x || xs < a->n || xs % 4 || ((uintptr_t)x & 15) || ((uintptr_t)a->q & 15))
+        return fail(PK_HIP_EINVAL, "quantize_dev: x and q 16-byte aligned, xs >= n and a multiple of 4");
+    return launch_quant(a, x, xs, (hipStream_t)stream);
+}
+
+int pk_hip_gemm_q8_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
+                       const float *ws, const float *bias, const pk_hip_act *a, int add, int rmode,
+                       void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!m)
+        return fail(PK_HIP_ENOTUP, "gemm_q8_dev: no matrix");
+    if ((e = check_act(a, true)))
+        return e;
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!out || !ws)
+        return fail(PK_HIP_EINVAL, "gemm_q8_dev: out or ws is NULL");
+    if ((uintptr_t)a->q & 15)
+        return fail(PK_HIP_EINVAL, "gemm_q8_dev: a->q must be 16-byte aligned");
+    if (a->T > 1 && os < rows)
+        return fail(PK_HIP_EINVAL, "gemm_q8_dev: output stride %zu is under rows %u", os, rows);
+    if (rmode < 0 || rmode > 3)
+        return fail(PK_HIP_EROUND, "gemm_q8_dev: rmode %d", rmode);
+    if ((e = check_panel(m, r0, rows, a->n)))
+        return e;
+    return launch_product(out, os, m, r0, rows, ws, bias, a, add, rmode, (hipStream_t)stream);
+}
+
+int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, const float *ws,
+                               const float *bias, const pk_hip_seg *segs, uint32_t nseg, int add,
+                               void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!m)
+        return fail(PK_HIP_ENOTUP, "gemm_q8_grouped_dev: no matrix");
+    if (!segs || nseg == 0 || nseg > (uint32_t)pkq8::kMaxSegs)
+        return fail(PK_HIP_EINVAL, "gemm_q8_grouped_dev: nseg %u is not in [1, %d]", nseg, pkq8::kMaxSegs);
+    if (!ws)
+        return fail(PK_HIP_EINVAL, "gemm_q8_grouped_dev: ws is NULL");
+    const uint32_t n = segs[0].a.n, qb = segs[0].a.qb;
+    pkq8::SegTable tab;
+    tab.nseg = 0;
+    for (uint32_t i = 0; i < nseg; i++) {
+        const pk_hip_seg &sg = segs[i];
+        if ((e = check_act(&sg.a, true)))
+            return e;
+        if (sg.a.T == 0)
+            continue;
+        if (sg.a.n != n || sg.a.qb != qb)
+            return fail(PK_HIP_EINVAL, "gemm_q8_grouped_dev: segment %u has n %u qb %u, not %u %u", i,
+                        sg.a.n, sg.a.qb, n, qb);
+        if (!sg.out || ((uintptr_t)sg.a.q & 15) || (sg.a.T > 1 && sg.os < rows))
+            return fail(PK_HIP_EINVAL, "gemm_q8_grouped_dev: segment %u: out NULL, q unaligned or os < rows", i);
+        tab.s[tab.nseg++] = pkq8::Seg{ sg.out, sg.a.q, sg.a.d, (uint64_t)sg.os, sg.a.T, 0 };
+    }
+    if (tab.nseg == 0)
+        return PK_HIP_OK;
+    if ((e = check_panel(m, r0, rows, n)))
+        return e;
+    pkq8::GemmArgs g;
+    g.w = m->w + (size_t)(r0 / 16) * m->ku * pkq8::kUnitBytes;
+    g.ws = ws;
+    g.bias = bias;
+    g.rows = rows;
+    g.n = n;
+    g.ku = m->ku;
+    g.qb = qb;
+    g.nb = n / qb;
+    g.add = add;
+    g.rmode = 0;
+    const char *name = "";
+    if (pkq8::launch_gemm(g, tab, (hipStream_t)stream, &name))
+        return hip_fail(hipGetLastError(), "gemm_q8_grouped launch");
+    g_kernel = name;
+    return PK_HIP_OK;
+}
+
+}  // extern "C"

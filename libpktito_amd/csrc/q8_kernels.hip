@@ -1,0 +1,624 @@
+/* The int8 product path on gfx950: the quantizer, the weight repack, and the
+ * int8 product with its fp32 epilogue.
+ *
+ * Bits. Every result is the reference's ref backend's
+ * (backend/ref/kernels.c:24-86 in peterheb/libpktito): integer sums are
+ * exact in any order, so the MFMAs may take the inputs in whatever order
+ * their lanes hold them, and the few float operations a block or an output
+ * has are written out one by one in ref's order. The file is built with
+ * -ffp-contract=off and the pragma below, so that no multiply and add the
+ * code keeps apart is fused, and without any flag that flushes denormals
+ * (a block's scale can be subnormal) or relaxes division.
+ */
+#include "q8_internal.h"
+
+#include <float.h>
+#include <stdio.h>
+
+#pragma clang fp contract(off)
+
+namespace pkq8 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+/* ------------------------------------------------------------ quantize --
+ *
+ * backend/ref/kernels.c:24-58, per column t and block b of qb inputs:
+ *   a NaN in the block, an infinite amax, or amax < 2^-121  ->  d = +0, q = 0
+ *   otherwise d = amax / 127, id = 127 / amax, q = rint(x * id)
+ * amax is a max, the same in any order. Both divisions are IEEE divisions
+ * (hipcc's default correctly rounded fp32 divide), rint is v_rndne_f32. */
+
+__device__ __forceinline__ int q1(float v, float id) { return (int)__builtin_rintf(v * id); }
+
+__device__ __forceinline__ int pack4(float4 v, float id) {
+    return (q1(v.x, id) & 0xff) | (q1(v.y, id) & 0xff) << 8 | (q1(v.z, id) & 0xff) << 16 |
+           (q1(v.w, id) & 0xff) << 24;
+}
+
+__device__ __forceinline__ void absmax4(float4 v, float &amax, int &nan) {
+    nan |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+    amax = fmaxf(amax, fabsf(v.x));
+    amax = fmaxf(amax, fabsf(v.y));
+    amax = fmaxf(amax, fabsf(v.z));
+    amax = fmaxf(amax, fabsf(v.w));
+}
+
+__device__ __forceinline__ bool zero_block(float amax, int nan) {
+    return nan || !__builtin_isfinite(amax) || amax < 0x1p-121f;
+}
+
+/* A whole column is one block (qb == n, "per-row" quantization): one
+ * workgroup of W waves a column, each thread up to CH chunks of 16 inputs,
+ * held in registers between the max and the rounding. */
+template <int W, int CH>
+__global__ __launch_bounds__(64 * W) void quant_col_kernel(int8_t *__restrict__ q, float *__restrict__ d,
+                                                           const float *__restrict__ x, size_t xs,
+                                                           uint32_t n) {
+    const uint32_t t = blockIdx.x, nch = n >> 4;
+    const float *xr = x + (size_t)t * xs;
+    float4 v[CH][4];
+    float amax = 0.0f;
+    int nan = 0;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t ch = threadIdx.x + c * 64 * W;
+        if (ch < nch) {
+            const float4 *p = (const float4 *)(xr + (size_t)ch * 16);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[c][e] = p[e];
+                absmax4(v[c][e], amax, nan);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        nan |= __shfl_xor(nan, off, 64);
+    }
+    if (W > 1) {
+        __shared__ float sm[W];
+        __shared__ int sn[W];
+        if ((threadIdx.x & 63) == 0) {
+            sm[threadIdx.x >> 6] = amax;
+            sn[threadIdx.x >> 6] = nan;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < W; i++) {
+            amax = fmaxf(amax, sm[i]);
+            nan |= sn[i];
+        }
+    }
+    const bool zero = zero_block(amax, nan);
+    float dv = 0.0f, id = 0.0f;
+    if (!zero) {
+        dv = amax / 127.0f;
+        id = 127.0f / amax;
+    }
+    int8_t *qr = q + (size_t)t * n;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t ch = threadIdx.x + c * 64 * W;
+        if (ch < nch) {
+            v4i o = {0, 0, 0, 0};
+            if (!zero)
+                o = v4i{pack4(v[c][0], id), pack4(v[c][1], id), pack4(v[c][2], id),
+                        pack4(v[c][3], id)};
+            *(v4i *)(qr + (size_t)ch * 16) = o;
+        }
+    }
+    if (threadIdx.x == 0)
+        d[t] = dv;
+}
+
+/* Blocks of qb = 16 * G inputs, G a power of two up to 64: one thread a
+ * chunk of 16, a block's G threads adjacent lanes of one wave. */
+template <int G>
+__global__ __launch_bounds__(256) void quant_blk_kernel(int8_t *__restrict__ q, float *__restrict__ d,
+                                                        const float *__restrict__ x, size_t xs,
+                                                        uint32_t n, uint32_t T) {
+    const uint32_t nch = n >> 4, nb = nch / G;
+    const uint64_t total = (uint64_t)T * nch;
+    uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool live = c < total;
+    if (!live)
+        c = total - 1;      /* a whole group is past the end or none of it is */
+    const uint32_t t = (uint32_t)(c / nch), ch = (uint32_t)(c % nch);
+    const float4 *p = (const float4 *)(x + (size_t)t * xs + (size_t)ch * 16);
+    float4 v[4];
+    float amax = 0.0f;
+    int nan = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        v[e] = p[e];
+        absmax4(v[e], amax, nan);
+    }
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        nan |= __shfl_xor(nan, off, 64);
+    }
+    if (!live)
+        return;
+    const bool zero = zero_block(amax, nan);
+    float dv = 0.0f, id = 0.0f;
+    if (!zero) {
+        dv = amax / 127.0f;
+        id = 127.0f / amax;
+    }
+    v4i o = {0, 0, 0, 0};
+    if (!zero)
+        o = v4i{pack4(v[0], id), pack4(v[1], id), pack4(v[2], id), pack4(v[3], id)};
+    *(v4i *)(q + (size_t)t * n + (size_t)ch * 16) = o;
+    if (ch % G == 0)
+        d[(size_t)t * nb + ch / G] = dv;
+}
+
+/* Any other qb (a multiple of 32 that is neither the whole column nor
+ * 16 times a power of two): one thread a block, the reference's loop. */
+__global__ __launch_bounds__(256) void quant_any_kernel(int8_t *__restrict__ q, float *__restrict__ d,
+                                                        const float *__restrict__ x, size_t xs,
+                                                        uint32_t n, uint32_t qb, uint32_t T) {
+    const uint32_t nb = n / qb;
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint64_t)T * nb)
+        return;
+    const uint32_t t = (uint32_t)(i / nb), b = (uint32_t)(i % nb);
+    const float *v = x + (size_t)t * xs + (size_t)b * qb;
+    int8_t *qq = q + (size_t)t * n + (size_t)b * qb;
+    float amax = 0.0f;
+    int nan = 0;
+    for (uint32_t k = 0; k < qb; k++) {
+        nan |= v[k] != v[k];
+        amax = fmaxf(amax, fabsf(v[k]));
+    }
+    const bool zero = zero_block(amax, nan);
+    float dv = 0.0f, id = 0.0f;
+    if (!zero) {
+        dv = amax / 127.0f;
+        id = 127.0f / amax;
+    }
+    for (uint32_t k = 0; k < qb; k++)
+        qq[k] = zero ? 0 : (int8_t)q1(v[k], id);
+    d[i] = dv;
+}
+
+int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb,
+                    uint32_t T, hipStream_t s, const char **name) {
+    if (T == 0)
+        return 0;
+    const uint32_t nch = n / 16;
+    if (qb == n && nch <= 64) {
+        quant_col_kernel<1, 1><<<T, 64, 0, s>>>(q, d, x, xs, n);
+        *name = "quant_col<1,1>";
+    } else if (qb == n && nch <= 256) {
+        quant_col_kernel<4, 1><<<T, 256, 0, s>>>(q, d, x, xs, n);
+        *name = "quant_col<4,1>";
+    } else if (qb == n && nch <= 1024) {
+        quant_col_kernel<4, 4><<<T, 256, 0, s>>>(q, d, x, xs, n);
+        *name = "quant_col<4,4>";
+    } else {
+        const uint32_t g = qb / 16;
+        const uint64_t total = (uint64_t)T * nch;
+        const uint32_t grid = (uint32_t)((total + 255) / 256);
+        switch (g) {
+#define PK_G(G)                                                                    \
+    case G:                                                                        \
+        quant_blk_kernel<G><<<grid, 256, 0, s>>>(q, d, x, xs, n, T);               \
+        *name = "quant_blk<" #G ">";                                               \
+        break;
+            PK_G(2) PK_G(4) PK_G(8) PK_G(16) PK_G(32) PK_G(64)
+#undef PK_G
+        default: {
+            const uint64_t blocks = (uint64_t)T * (n / qb);
+            quant_any_kernel<<<(uint32_t)((blocks + 255) / 256), 256, 0, s>>>(q, d, x, xs, n, qb, T);
+            *name = "quant_any";
+        }
+        }
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+/* -------------------------------------------------------------- repack --
+ *
+ * PK_Q8 (core/pkf.h:28-41: q(r, k) at ((r/16)(cols/4) + k/4) 64 + (r%16) 4 +
+ * k%4) into units (q8_internal.h): one thread a 16-byte lane slot. */
+__global__ __launch_bounds__(256) void repack_kernel(int8_t *__restrict__ dst,
+                                                     const int8_t *__restrict__ src,
+                                                     uint32_t panels, uint32_t cols, uint32_t ku) {
+    const uint64_t slot = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (slot >= (uint64_t)panels * ku * 64)
+        return;
+    const uint32_t lane = (uint32_t)(slot & 63);
+    const uint64_t unit = slot >> 6;
+    const uint32_t p = (uint32_t)(unit / ku), u = (uint32_t)(unit % ku);
+    const uint32_t r = lane & 15, kq = lane >> 4;
+    const uint32_t k0 = u * 64 + kq * 16;
+    int o[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const uint32_t k = k0 + 4 * g;
+        o[g] = k < cols ? *(const int *)(src + ((size_t)p * (cols / 4) + k / 4) * 64 + r * 4) : 0;
+    }
+    *(v4i *)(dst + slot * 16) = v4i{o[0], o[1], o[2], o[3]};
+}
+
+int launch_repack(int8_t *dst, const int8_t *src, uint32_t rows, uint32_t cols, hipStream_t s) {
+    const uint32_t panels = rows / 16, ku = units_per_panel(cols);
+    const uint64_t slots = (uint64_t)panels * ku * 64;
+    if (slots == 0)
+        return 0;
+    repack_kernel<<<(uint32_t)((slots + 255) / 256), 256, 0, s>>>(dst, src, panels, cols, ku);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+/* ------------------------------------------------------------- product --
+ *
+ * out[t * os + r] (backend/kernels.h:60-78):
+ *   acc = 0; per block b in order: s = exact int32 sum, acc = fmaf((float)s, d[t][b], acc)
+ *   v = acc * ws[r]; if bias: v = v + bias[r]; out = add ? out + v : v
+ *
+ * The MFMA is v_mfma_i32_16x16x64_i8 with the weights as its A operand and
+ * the activations as its B: a 16x16 tile's lane l holds output row (frame)
+ * t = l % 16 and the four consecutive channels r = 4 (l / 16) + i, so the
+ * epilogue reads one scale d[t] a tile and writes a float4 a lane. Both
+ * operands come from LDS in the unit layout, one ds_read_b128 a lane a
+ * 16x64 fragment, lanes in address order.
+ *
+ * A workgroup is WN x WM waves; each wave TN x TM tiles of 16x16: the
+ * workgroup's tile is 16 TN WN channels by 16 TM WM frames. Inputs move in
+ * stages of 64, double-buffered through LDS: each thread loads its share of
+ * the next stage into registers with 128-bit global loads while the MFMAs
+ * run on this one, then stores it to the other buffer.
+ *
+ * MODE 0: one block a column (qb == n): the int32 sums run over the whole
+ *         input, and the epilogue's first operation is fmaf(s, d, +0).
+ * MODE 1: blocks of a multiple of 64: each block's sums are turned into the
+ *         float chain at the stage that ends it.
+ * MODE 2: blocks of an odd multiple of 32: the 16x16x32 MFMA on each half
+ *         stage, the chain updated at every block's end.
+ *
+ * Rows past the matrix and frames past T are clamped to the last one when
+ * loaded (and never stored); inputs past n read a column's first inputs,
+ * which meet the repacked matrix's zero padding, so every load is in bounds
+ * and adds nothing. */
+
+template <int WN, int WM, int TN, int TM, int MODE>
+__device__ __forceinline__ void gemm_tile(const GemmArgs &g, const Seg &sg, uint32_t tn, uint32_t tm) {
+    constexpr int NW = WN * WM;
+    constexpr int BN = 16 * TN * WN, BM = 16 * TM * WM;
+    constexpr int UB = BN / 16, UA = BM / 16, UNITS = UA + UB;
+    static_assert(UNITS % NW == 0, "each wave loads whole units");
+    constexpr int LPW = UNITS / NW;
+    constexpr int FN = MODE == 0 ? 1 : TN, FM = MODE == 0 ? 1 : TM;
+    __shared__ __attribute__((aligned(16))) int8_t lds[2][UNITS * kUnitBytes];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wn = wave % WN, wm = wave / WN;
+    const uint32_t T = sg.T;
+    const uint32_t n0 = tn * BN, m0 = tm * BM;
+    const uint32_t npan = g.rows >> 4;
+    const uint32_t n = g.n, ku = g.ku;
+
+    if (g.rmode)
+        __builtin_amdgcn_s_setreg(2049, g.rmode);    /* MODE.FP_ROUND, single precision */
+
+    /* this thread's load slots: units [wave * LPW, wave * LPW + LPW) of a stage,
+     * the weight units first */
+    const int8_t *src[LPW];
+    bool isw[LPW];
+#pragma unroll
+    for (int s = 0; s < LPW; s++) {
+        const int u = wave * LPW + s;
+        if (u < UB) {
+            uint32_t p = n0 / 16 + u;
+            p = p < npan ? p : npan - 1;
+            src[s] = g.w + (size_t)p * ku * kUnitBytes + lane * 16;
+            isw[s] = true;
+        } else {
+            uint32_t row = m0 + (u - UB) * 16 + (lane & 15);
+            row = row < T ? row : T - 1;
+            src[s] = sg.q + (size_t)row * n;
+            isw[s] = false;
+        }
+    }
+
+    v4i stage[LPW];
+    auto gload = [&](uint32_t kt) {
+#pragma unroll
+        for (int s = 0; s < LPW; s++) {
+            if (isw[s]) {
+                stage[s] = *(const v4i *)(src[s] + (size_t)kt * kUnitBytes);
+            } else {
+                /* inputs past n: the row's first 16, against zero weights */
+                const uint32_t k = kt * 64 + (lane >> 4) * 16;
+                stage[s] = *(const v4i *)(src[s] + (k < n ? k : 0));
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int s = 0; s < LPW; s++)
+            *(v4i *)(&lds[buf][(wave * LPW + s) * kUnitBytes + lane * 16]) = stage[s];
+    };
+
+    v4i acc[TN][TM];
+    float accf[FN][FM][4];
+#pragma unroll
+    for (int i = 0; i < TN; i++)
+#pragma unroll
+        for (int j = 0; j < TM; j++)
+            acc[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                accf[i][j][r] = 0.0f;
+
+    /* this lane's frame in each tile column j, clamped for the loads */
+    uint32_t tj[TM];
+#pragma unroll
+    for (int j = 0; j < TM; j++) {
+        const uint32_t t = m0 + (wm * TM + j) * 16 + (lane & 15);
+        tj[j] = t < T ? t : T - 1;
+    }
+
+    /* block b's sums into the float chain (ref's acc = fmaf((float)s, d, acc)),
+     * and the sums back to zero */
+    auto chain = [&](uint32_t b) {
+        if (MODE != 0) {
+#pragma unroll
+            for (int j = 0; j < TM; j++) {
+                const float dt = sg.d[(size_t)tj[j] * g.nb + b];
+#pragma unroll
+                for (int i = 0; i < TN; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        float &f = accf[MODE == 0 ? 0 : i][MODE == 0 ? 0 : j][r];
+                        f = __builtin_fmaf((float)acc[i][j][r], dt, f);
+                        acc[i][j][r] = 0;
+                    }
+            }
+        }
+    };
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (uint32_t kt = 0; kt < ku; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < ku)
+            gload(kt + 1);
+        const int8_t *lb = &lds[cur][0];
+        if (MODE != 2) {
+            v4i wf[TN], af[TM];
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+                wf[i] = *(const v4i *)(lb + (wn * TN + i) * kUnitBytes + lane * 16);
+#pragma unroll
+            for (int j = 0; j < TM; j++)
+                af[j] = *(const v4i *)(lb + (UB + wm * TM + j) * kUnitBytes + lane * 16);
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+#pragma unroll
+                for (int j = 0; j < TM; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[i], af[j], acc[i][j], 0, 0, 0);
+            if (MODE == 1) {
+                const uint32_t kend = (kt + 1) * 64;
+                if (kend <= n && kend % g.qb == 0)
+                    chain(kend / g.qb - 1);
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                /* half h of the stage: 32 inputs, 8 bytes a lane, the same
+                 * bytes of both operands */
+                const int off = ((2 * h + (lane >> 5)) * 16 + (lane & 15)) * 16 + ((lane >> 4) & 1) * 8;
+                long wf[TN], af[TM];
+#pragma unroll
+                for (int i = 0; i < TN; i++)
+                    wf[i] = *(const long *)(lb + (wn * TN + i) * kUnitBytes + off);
+#pragma unroll
+                for (int j = 0; j < TM; j++)
+                    af[j] = *(const long *)(lb + (UB + wm * TM + j) * kUnitBytes + off);
+#pragma unroll
+                for (int i = 0; i < TN; i++)
+#pragma unroll
+                    for (int j = 0; j < TM; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf[i], af[j], acc[i][j], 0, 0, 0);
+                const uint32_t kend = kt * 64 + 32 * (h + 1);
+                if (kend <= n && kend % g.qb == 0)
+                    chain(kend / g.qb - 1);
+            }
+        }
+        if (kt + 1 < ku)
+            lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    /* the epilogue: ref's operations in ref's order, four channels a lane */
+    const bool vec = ((sg.os & 3) == 0) && ((((uintptr_t)sg.out) & 15) == 0);
+#pragma unroll
+    for (int j = 0; j < TM; j++) {
+        const uint32_t t = m0 + (wm * TM + j) * 16 + (lane & 15);
+        if (t >= T)
+            continue;
+        const float dt = MODE == 0 ? sg.d[t] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TN; i++) {
+            const uint32_t c = n0 + (wn * TN + i) * 16 + (lane >> 4) * 4;
+            if (c >= g.rows)
+                continue;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float a = MODE == 0 ? __builtin_fmaf((float)acc[i][j][r], dt, 0.0f)
+                                          : accf[MODE == 0 ? 0 : i][MODE == 0 ? 0 : j][r];
+                v[r] = a * g.ws[c + r];
+                if (g.bias)
+                    v[r] = v[r] + g.bias[c + r];
+            }
+            float *o = sg.out + (size_t)t * sg.os + c;
+            if (vec) {
+                float4 ov = make_float4(v[0], v[1], v[2], v[3]);
+                if (g.add) {
+                    const float4 old = *(const float4 *)o;
+                    ov.x = old.x + ov.x;
+                    ov.y = old.y + ov.y;
+                    ov.z = old.z + ov.z;
+                    ov.w = old.w + ov.w;
+                }
+                *(float4 *)o = ov;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    o[r] = g.add ? o[r] + v[r] : v[r];
+            }
+        }
+    }
+}
+
+/* One product: tiles with channels fastest, so neighbouring workgroups share
+ * their frames' inputs. */
+template <int WN, int WM, int TN, int TM, int MODE>
+__global__ __launch_bounds__(64 * WN * WM) void gemm_q8_kernel(GemmArgs g, Seg sg, uint32_t tiles_n) {
+    gemm_tile<WN, WM, TN, TM, MODE>(g, sg, blockIdx.x % tiles_n, blockIdx.x / tiles_n);
+}
+
+/* A grouped product: the segments' frame tiles one after another, each
+ * workgroup finding its segment in the table. */
+template <int WN, int WM, int TN, int TM, int MODE>
+__global__ __launch_bounds__(64 * WN * WM) void gemm_q8_grouped_kernel(GemmArgs g, SegTable tab,
+                                                                       uint32_t tiles_n) {
+    const uint32_t tm = blockIdx.x / tiles_n;
+    uint32_t i = 0;
+    while (i + 1 < tab.nseg && tab.s[i + 1].tile0 <= tm)
+        i++;
+    gemm_tile<WN, WM, TN, TM, MODE>(g, tab.s[i], blockIdx.x % tiles_n, tm - tab.s[i].tile0);
+}
+
+/* The skinny product, a few frames (T <= 16): bound by streaming the weights
+ * once. A workgroup takes one 16-row panel; its KW waves split the panel's
+ * units between them, each reading its weight units straight from HBM (1 KB
+ * contiguous a wave a unit) and the frames' inputs from L2, and their int32
+ * sums meet in LDS. Per-row blocks only (MODE 0). */
+template <int KW>
+__global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg sg) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t p = blockIdx.x, n = g.n, ku = g.ku, T = sg.T;
+    if (g.rmode)
+        __builtin_amdgcn_s_setreg(2049, g.rmode);
+    const int8_t *wp = g.w + (size_t)p * ku * kUnitBytes + lane * 16;
+    uint32_t row = lane & 15;
+    row = row < T ? row : T - 1;
+    const int8_t *ap = sg.q + (size_t)row * n;
+    v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+    uint32_t u = wave;
+    for (; u + KW < ku; u += 2 * KW) {
+        const v4i w0 = *(const v4i *)(wp + (size_t)u * kUnitBytes);
+        const v4i w1 = *(const v4i *)(wp + (size_t)(u + KW) * kUnitBytes);
+        const uint32_t k0 = u * 64 + (lane >> 4) * 16, k1 = k0 + KW * 64;
+        const v4i a0 = *(const v4i *)(ap + (k0 < n ? k0 : 0));
+        const v4i a1 = *(const v4i *)(ap + (k1 < n ? k1 : 0));
+        acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0, a0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w1, a1, acc1, 0, 0, 0);
+    }
+    if (u < ku) {
+        const v4i w0 = *(const v4i *)(wp + (size_t)u * kUnitBytes);
+        const uint32_t k0 = u * 64 + (lane >> 4) * 16;
+        const v4i a0 = *(const v4i *)(ap + (k0 < n ? k0 : 0));
+        acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0, a0, acc0, 0, 0, 0);
+    }
+    __shared__ v4i red[KW][64];
+    red[wave][lane] = acc0 + acc1;
+    __syncthreads();
+    if (wave != 0)
+        return;
+    v4i s = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < KW; w++)
+        s += red[w][lane];
+    const uint32_t t = lane & 15;
+    if (t >= T)
+        return;
+    const float dt = sg.d[t];
+    const uint32_t c = p * 16 + (lane >> 4) * 4;
+    float *o = sg.out + (size_t)t * sg.os + c;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float v = __builtin_fmaf((float)s[r], dt, 0.0f) * g.ws[c + r];
+        if (g.bias)
+            v = v + g.bias[c + r];
+        o[r] = g.add ? o[r] + v : v;
+    }
+}
+
+template <int WN, int WM, int TN, int TM, int MODE>
+static void run_tiled(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
+    constexpr uint32_t BN = 16 * TN * WN, BM = 16 * TM * WM;
+    const uint32_t tiles_n = (g.rows + BN - 1) / BN;
+    if (tab.nseg == 1) {
+        const uint32_t tiles_m = (tab.s[0].T + BM - 1) / BM;
+        gemm_q8_kernel<WN, WM, TN, TM, MODE><<<tiles_n * tiles_m, 64 * WN * WM, 0, s>>>(g, tab.s[0], tiles_n);
+    } else {
+        SegTable t = tab;
+        uint32_t tiles = 0;
+        for (uint32_t i = 0; i < t.nseg; i++) {
+            t.s[i].tile0 = tiles;
+            tiles += (t.s[i].T + BM - 1) / BM;
+        }
+        gemm_q8_grouped_kernel<WN, WM, TN, TM, MODE><<<tiles_n * tiles, 64 * WN * WM, 0, s>>>(g, t, tiles_n);
+    }
+}
+
+template <int WN, int WM, int TN, int TM>
+static void run_mode(const GemmArgs &g, const SegTable &tab, hipStream_t s, int mode) {
+    if (mode == 0)
+        run_tiled<WN, WM, TN, TM, 0>(g, tab, s);
+    else if (mode == 1)
+        run_tiled<WN, WM, TN, TM, 1>(g, tab, s);
+    else
+        run_tiled<WN, WM, TN, TM, 2>(g, tab, s);
+}
+
+int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const char **name) {
+    uint64_t frames = 0;
+    uint32_t tmax = 0;
+    for (uint32_t i = 0; i < tab.nseg; i++) {
+        frames += tab.s[i].T;
+        tmax = tab.s[i].T > tmax ? tab.s[i].T : tmax;
+    }
+    if (frames == 0 || g.rows == 0)
+        return 0;
+    const int mode = g.qb == g.n ? 0 : g.qb % 64 == 0 ? 1 : 2;
+    static const char *const modes[] = { "per-column", "blocks of 64k", "blocks of 32k" };
+    static thread_local char buf[96];
+    if (mode == 0 && tab.nseg == 1 && tmax <= 16) {
+        const uint32_t panels = g.rows / 16;
+        if (g.ku >= 32) {
+            gemm_q8_skinny_kernel<8><<<panels, 512, 0, s>>>(g, tab.s[0]);
+            *name = "skinny<8>";
+        } else {
+            gemm_q8_skinny_kernel<4><<<panels, 256, 0, s>>>(g, tab.s[0]);
+            *name = "skinny<4>";
+        }
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    /* 128 x 128 tiles where they fill the chip, 64 x 64 where they do not */
+    const uint64_t big = (uint64_t)((g.rows + 127) / 128) * ((frames + 127) / 128);
+    if (big >= 256) {
+        run_mode<2, 2, 4, 4>(g, tab, s, mode);
+        snprintf(buf, sizeof buf, "tiled<128x128> %s", modes[mode]);
+    } else {
+        run_mode<2, 2, 2, 2>(g, tab, s, mode);
+        snprintf(buf, sizeof buf, "tiled<64x64> %s", modes[mode]);
+    }
+    *name = buf;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace pkq8

@@ -1,0 +1,156 @@
+"""The device-resident path (activations and outputs in HBM, asynchronous on a
+stream) and the grouped launch, against the oracle bit for bit: the shapes
+of one FastConformer layer at a minute of audio and at ten minutes, and a
+ragged batch of segments in one launch."""
+import sys
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from libpktito_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    assert torch.cuda.is_available()
+    return torch
+
+
+def sampled_oracle(q, d, w, ws, bias, K, N, frames, add=0, old=None):
+    """The oracle's outputs for the given frames only (a sub-act of them)."""
+    idx = np.asarray(frames)
+    qs = np.ascontiguousarray(q.reshape(-1, K)[idx]).reshape(-1)
+    ds = np.ascontiguousarray(d[idx])
+    out = old[idx].reshape(-1).copy() if old is not None else np.zeros(len(idx) * N, np.float32)
+    ol.gemm_q8(out, N, w, ws, bias, N, qs, ds, K, K, len(idx), add, threads=16)
+    return out.reshape(len(idx), N)
+
+
+def run_product(pk, torch, name, M, K, N, half, add, seed, sample=64):
+    g = synth.rng(seed)
+    wr = synth.weights(g, N, K)
+    w = synth.pack_q8(wr)
+    ws = synth.scales(g, N)
+    x = synth.activations(g, M, K, half)
+    old = g.standard_normal((M, N)).astype(np.float32) if add else None
+    dev = torch.device("cuda")
+    xt = torch.from_numpy(x).to(dev)
+    qt = torch.empty((M, K), dtype=torch.int8, device=dev)
+    dt = torch.empty((M,), dtype=torch.float32, device=dev)
+    ot = torch.from_numpy(old).to(dev) if add else torch.empty((M, N), dtype=torch.float32, device=dev)
+    say("device product", name, M, K, N, add)
+    with pk.Q8Matrix(w, ws) as m:
+        pk.quantize_dev(qt, dt, xt, K, K, M, K)
+        pk.gemm_q8_dev(ot, N, m, 0, N, None, None, qt, dt, K, K, M, add, ws_ptr=m.dev_scales)
+        torch.cuda.synchronize()
+        say("kernel", pk.last_kernel())
+    q = qt.cpu().numpy().reshape(-1)
+    d = dt.cpu().numpy()
+    out = ot.cpu().numpy()
+    q2, d2 = ol.quantize(x.reshape(-1), M, K, K, K)
+    assert np.array_equal(q, q2) and np.array_equal(bits(d), bits(d2)), name
+    frames = np.unique(np.concatenate([[0, M - 1], synth.rng(seed + 1).integers(0, M, sample)]))
+    want = sampled_oracle(q, d, w, ws, None, K, N, frames, add, old)
+    assert np.array_equal(bits(out[frames]), bits(want)), name
+
+
+@pytest.mark.parametrize("prod", synth.layer_products(750), ids=lambda p: p[0])
+def test_layer_products_minute(hip, torch, prod):
+    name, M, K, N, half, add = prod
+    run_product(hip, torch, name, M, K, N, half, int(add), seed=zlib.crc32(name.encode()) % 1000)
+
+
+@pytest.mark.parametrize("prod", [p for p in synth.layer_products(7500) if p[0] in ("ff1_up", "ff1_down", "pos", "pw1")],
+                         ids=lambda p: p[0])
+def test_layer_products_ten_minutes(hip, torch, prod):
+    name, M, K, N, half, add = prod
+    run_product(hip, torch, name, M, K, N, half, int(add), seed=17 + len(name), sample=48)
+
+
+@pytest.mark.parametrize("K,N", [(1024, 4096), (4096, 1024)])
+def test_ragged_batch_grouped(hip, torch, K, N):
+    """Eight segments of 150-750 frames (12-60 s) in one launch: each
+    segment's outputs are the bits of its own product, and the oracle's."""
+    lens = synth.ragged_lengths()
+    g = synth.rng(K + N)
+    w = synth.pack_q8(synth.weights(g, N, K))
+    ws = synth.scales(g, N)
+    dev = torch.device("cuda")
+    segs, solo, host = [], [], []
+    with hip.Q8Matrix(w, ws) as m:
+        for L in lens:
+            x = synth.activations(g, L, K)
+            q, d = ol.quantize(x.reshape(-1), L, K, K, K)
+            qt = torch.from_numpy(q.reshape(L, K)).to(dev)
+            dt = torch.from_numpy(d).to(dev)
+            ot = torch.full((L, N), 7.0, dtype=torch.float32, device=dev)
+            o2 = torch.full((L, N), 7.0, dtype=torch.float32, device=dev)
+            segs.append((ot, N, qt, dt, K, K, L))
+            solo.append((o2, qt, dt, L))
+            host.append((q, d, L))
+        say("grouped", lens, K, N)
+        hip.gemm_q8_grouped_dev(m, 0, N, m.dev_scales, None, segs, 0)
+        for o2, qt, dt, L in solo:
+            hip.gemm_q8_dev(o2, N, m, 0, N, None, None, qt, dt, K, K, L, 0, ws_ptr=m.dev_scales)
+        torch.cuda.synchronize()
+    for (ot, _, _, _, _, _, L), (o2, _, _, _), (q, d, _) in zip(segs, solo, host):
+        a, b = ot.cpu().numpy(), o2.cpu().numpy()
+        assert np.array_equal(bits(a), bits(b))
+        frames = np.unique(np.concatenate([[0, L - 1], synth.rng(L).integers(0, L, 24)]))
+        want = sampled_oracle(q, d, w, ws, None, K, N, frames)
+        assert np.array_equal(bits(a[frames]), bits(want))
+
+
+def test_interior_panels_device(hip, torch):
+    """A run of panels from the middle of an uploaded matrix (r0 > 0) on the
+    device path, with bias and add, at an odd output stride."""
+    g = synth.rng(99)
+    M, K, N = 200, 1024, 512
+    w = synth.pack_q8(synth.weights(g, N, K))
+    ws = synth.scales(g, N)
+    bias = g.standard_normal(N).astype(np.float32)
+    x = synth.activations(g, M, K).reshape(-1)
+    q, d = ol.quantize(x, M, K, K, K)
+    os_ = N + 5
+    old = g.standard_normal(M * os_).astype(np.float32)
+    r0, rows = 144, 240
+    want = old.copy()
+    ol.gemm_q8(want, os_, w, ws, bias, rows, q, d, K, K, M, 1, r0=r0)
+    dev = torch.device("cuda")
+    ot = torch.from_numpy(old).to(dev)
+    qt, dt = torch.from_numpy(q).to(dev), torch.from_numpy(d).to(dev)
+    bt = torch.from_numpy(bias).to(dev)
+    wst = torch.from_numpy(ws).to(dev)
+    say("interior panels", r0, rows)
+    with hip.Q8Matrix(w, ws) as m:
+        hip.gemm_q8_dev(None, os_, m, r0, rows, None, None, qt, dt, K, K, M, 1,
+                        ws_ptr=wst.data_ptr() + 4 * r0, out_ptr=ot.data_ptr() + 4 * r0)
+        torch.cuda.synchronize()
+        # the same with a bias (its pointer at row r0)
+        ot2 = torch.from_numpy(old).to(dev)
+        import libpktito_amd as pk
+        a = pk.Act(qt.data_ptr(), dt.data_ptr(), K, K, M)
+        import ctypes
+        rc = pk.lib().pk_hip_gemm_q8_dev(ot2.data_ptr() + 4 * r0, os_, m.handle, r0, rows,
+                                         wst.data_ptr() + 4 * r0, bt.data_ptr() + 4 * r0,
+                                         ctypes.byref(a), 1, 0, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+    assert np.array_equal(bits(ot2.cpu().numpy()), bits(want))
+    want_nob = old.copy()
+    ol.gemm_q8(want_nob, os_, w, ws, None, rows, q, d, K, K, M, 1, r0=r0)
+    assert np.array_equal(bits(ot.cpu().numpy()), bits(want_nob))
