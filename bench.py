@@ -1,0 +1,518 @@
+"""The int8 product path on one MI355X: throughput of one FastConformer layer's
+int8 products, with the roofline of its dominant kernel and a CPU baseline.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu]
+
+A step is one pass of the hot path over one layer at a minute of audio: the
+eleven int8 products of a FastConformer layer (d_model 1024, feed-forward
+4096, 8 heads, the convolution module's pointwise 2048) at M = 750 frames
+(2M - 1 = 1499 for the positions' projection), each input quantized per row
+to int8 and multiplied with exact int32 sums into fp32 outputs by the
+reference's epilogue. Weights, scales and fp32 inputs are synthetic (int8
+uniform [-127, 127], scales uniform [1e-3, 1e-2], N(0, 1) inputs, half-normal
+into the down projections) and resident in HBM before the timed region. The
+22 launches of a step are captured once into a HIP graph and replayed; K
+replays are timed with events on the stream they run on.
+
+Printed: one JSON line. `value` is TOPS (2 M K N over the step's time). The
+`extra` object adds the long-form layer (M = 7500) and a ragged batch of 8
+segments in grouped launches, the 24-layer chained encoder sweep in ms per
+audio-minute, and the skinny (M <= 16) shapes against HBM. `cpu_baseline`
+times the reference's own backends (compiled from its sources into
+oracle/_ref) on the host's cores, on the same inputs.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_INT8_PEAK_TOPS = 5000.0      # MI355X dense int8, published
+HBM_PEAK_GBS = 8000.0             # MI355X HBM3E, published
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--quick", action="store_true", help="the layer only: no extras, no CPU baseline")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=8.0)
+    p.add_argument("--profile-kernel", default=None,
+                   help="only launch the dominant kernel's timing loop (for rocprofv3 --pmc runs)")
+    return p.parse_args()
+
+
+# --------------------------------------------------------------- device ---
+
+class Product:
+    """One int8 product of the layer, resident in HBM: its uploaded matrix, its
+    fp32 input, and its quantized activations and fp32 output buffers."""
+
+    def __init__(self, pk, torch, name, M, K, N, half, add, g, x_dev=None, xs=None, ws_gain=1.0):
+        from libpktito_amd import synth
+        self.name, self.M, self.K, self.N, self.add = name, M, K, N, int(add)
+        wr = synth.weights(g, N, K)
+        self.w = synth.pack_q8(wr)
+        self.ws = (synth.scales(g, N) * np.float32(ws_gain)).astype(np.float32)
+        self.m = pk.Q8Matrix(self.w, self.ws)
+        dev = torch.device("cuda")
+        if x_dev is None:
+            self.x_host = synth.activations(g, M, K, half)
+            self.x = torch.from_numpy(self.x_host).to(dev)
+            self.xs = K
+        else:
+            self.x_host = None
+            self.x, self.xs = x_dev, xs
+        self.q = torch.empty((M, K), dtype=torch.int8, device=dev)
+        self.d = torch.empty((M,), dtype=torch.float32, device=dev)
+        self.out = torch.zeros((M, N), dtype=torch.float32, device=dev)
+
+    def ops(self):
+        return 2.0 * self.M * self.K * self.N
+
+    def gemm_bytes(self):
+        M, K, N = self.M, self.K, self.N
+        return N * K + 4 * N + M * K + 4 * M + 4 * M * N + (4 * M * N if self.add else 0)
+
+    def quant_bytes(self):
+        return 4 * self.M * self.K + self.M * self.K + 4 * self.M
+
+    def quantize(self, pk, stream=None):
+        pk.quantize_dev(self.q, self.d, self.x, self.K, self.K, self.M, self.xs, stream=stream)
+
+    def gemm(self, pk, stream=None):
+        pk.gemm_q8_dev(self.out, self.N, self.m, 0, self.N, None, None, self.q, self.d, self.K, self.K,
+                       self.M, self.add, ws_ptr=self.m.dev_scales, stream=stream)
+
+
+def make_layer(pk, torch, M, seed, ws_gain=None):
+    from libpktito_amd import synth
+    g = synth.rng(seed)
+    prods = []
+    for (name, mm, K, N, half, add) in synth.layer_products(M):
+        gain = 1.0 if ws_gain is None else ws_gain(K)
+        prods.append(Product(pk, torch, name, mm, K, N, half, add, g, ws_gain=gain))
+    return prods
+
+
+def graph_of(torch, fn):
+    """fn's launches captured into a HIP graph on a side stream."""
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()        # once outside capture, so every lazy set-up has happened
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, reps, warmup):
+    """ms per replay of graph g: warmup replays, then reps replays between two
+    events on the current stream, synchronized on both sides."""
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def kernel_ms(pk, torch, prod, launches=64, reps=5):
+    """The average duration of one product's kernel: a graph of `launches`
+    back-to-back launches of it, timed with events on its stream."""
+    def fn():
+        for _ in range(launches):
+            prod.gemm(pk)
+    g = graph_of(torch, fn)
+    best = min(time_graph(torch, g, 3, 1) for _ in range(reps))
+    return best / launches
+
+
+# ------------------------------------------------------------ workloads ---
+
+def layer_step(pk, prods):
+    def fn():
+        for p in prods:
+            p.quantize(pk)
+            p.gemm(pk)
+    return fn
+
+
+def check_replay(pk, torch, prods, graph):
+    """A replay's outputs equal an eager step's, bit for bit (graphs replayed
+    several times with eager work between)."""
+    fn = layer_step(pk, prods)
+    for _ in range(3):
+        for p in prods:
+            p.out.zero_()
+        fn()
+        torch.cuda.synchronize()
+        eager = [p.out.clone() for p in prods]
+        for p in prods:
+            p.out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for p, e in zip(prods, eager):
+            if not torch.equal(p.out.view(torch.int32), e.view(torch.int32)):
+                return False
+    return True
+
+
+def encoder_sweep(pk, torch, M, seed):
+    """24 layers with independent weights (~0.6 GB of int8 in HBM),
+    each product's input the previous product's fp32 output re-quantized per
+    row, in the order ff1_up, ff1_down, q, k, v, o, pw1 (first 1024 of its 2048
+    columns into pw2), pw2, ff2_up, ff2_down; the positions' projection reads
+    the positional encodings, quantized once an encode as the reference does.
+    Each matrix's scales are the configs' uniform [1e-3, 1e-2] times
+    1 / (sqrt(K) * 73.6 * 0.0055) so that a chain of 264 products keeps its
+    activations finite (timing does not depend on the values)."""
+    from libpktito_amd import synth
+    dev = torch.device("cuda")
+    g = synth.rng(seed)
+    x0 = torch.from_numpy(synth.activations(g, M, 1024)).to(dev)
+    ape = torch.from_numpy(synth.activations(g, 2 * M - 1, 1024)).to(dev)
+    ape_q = torch.empty((2 * M - 1, 1024), dtype=torch.int8, device=dev)
+    ape_d = torch.empty((2 * M - 1,), dtype=torch.float32, device=dev)
+    gain = lambda K: 1.0 / (np.sqrt(K) * 73.6 * 0.0055)   # noqa: E731
+    order = ["ff1_up", "ff1_down", "q", "k", "v", "o", "pw1", "pw2", "ff2_up", "ff2_down"]
+    shapes = {p[0]: p for p in synth.layer_products(M)}
+    layers = []
+    prev = x0
+    prev_xs = 1024
+    for L in range(24):
+        lay = {}
+        for name in order:
+            _, mm, K, N, half, add = shapes[name]
+            p = Product(pk, torch, name, mm, K, N, half, add, g, x_dev=prev, xs=prev_xs, ws_gain=gain(K))
+            lay[name] = p
+            prev, prev_xs = p.out, N
+        _, mm, K, N, half, add = shapes["pos"]
+        pp = Product(pk, torch, "pos", mm, K, N, half, add, g, x_dev=ape, xs=1024, ws_gain=gain(K))
+        pp.q, pp.d = ape_q, ape_d
+        lay["pos"] = pp
+        layers.append(lay)
+        prev = lay["ff2_down"].out
+        prev_xs = 1024
+
+    def fn():
+        pk.quantize_dev(ape_q, ape_d, ape, 1024, 1024, 2 * M - 1, 1024)
+        for lay in layers:
+            for name in order[:5]:
+                lay[name].quantize(pk)
+                lay[name].gemm(pk)
+            lay["pos"].gemm(pk)
+            for name in order[5:]:
+                p = lay[name]
+                p.quantize(pk)
+                p.gemm(pk)
+    ops = sum(p.ops() for lay in layers for p in lay.values())
+    return fn, ops, layers
+
+
+def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20):
+    """M in {1, 4, 16} rows through weights rotated over more than
+    512 MB of distinct matrices, so that L2 and the 256 MB MALL serve none of
+    them. One graph of launches over the copies; GB/s from the algorithmic
+    bytes N K + 4 N + M K + 4 M + 4 M N of each launch."""
+    from libpktito_amd import synth
+    dev = torch.device("cuda")
+    out = []
+    for (K, N, real) in shapes:
+        per = N * K
+        copies = max(8, budget_bytes // per + 1)
+        g = synth.rng(K * 31 + N)
+        big = g.integers(-127, 128, size=copies * per, dtype=np.int8)
+        wsa = synth.scales(g, N)
+        mats = []
+        for c in range(copies):
+            wslice = big[c * per:(c + 1) * per]
+            mats.append(pk.Q8Matrix(wslice, wsa))
+        for M in (1, 4, 16):
+            x = torch.from_numpy(synth.activations(g, M, K)).to(dev)
+            q = torch.empty((M, K), dtype=torch.int8, device=dev)
+            d = torch.empty((M,), dtype=torch.float32, device=dev)
+            pk.quantize_dev(q, d, x, K, K, M, K)
+            o = torch.empty((M, N), dtype=torch.float32, device=dev)
+
+            def fn():
+                for m in mats:
+                    pk.gemm_q8_dev(o, N, m, 0, N, None, None, q, d, K, K, M, 0, ws_ptr=m.dev_scales)
+            gr = graph_of(torch, fn)
+            ms = min(time_graph(torch, gr, 2, 1) for _ in range(3)) / len(mats)
+            byts = N * K + 4 * N + M * K + 4 * M + 4 * M * N
+            out.append(dict(M=M, K=K, N=N, outputs=real, us=round(ms * 1e3, 3),
+                            GBs=round(byts / (ms * 1e-3) / 1e9, 1),
+                            hbm_frac=round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3),
+                            kernel=pk.last_kernel()))
+        for m in mats:
+            m.release()
+        del big
+    return out
+
+
+# --------------------------------------------------------- CPU baseline ---
+
+def cpu_baseline(prods_host, seconds):
+    """The reference's backends on this host's cores, on the layer's inputs:
+    each product quantized per row (16 frames an item) and multiplied in
+    64-row slices dealt from an atomic counter over every core
+    (tests/gemmbench.c:77-94, core/passes.c:28-46 in the reference)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+    cores = min(os.cpu_count() or 1, 64)
+    impls = []
+    if ol.ref() is not None:
+        for bid in ("avx512-vnni", "avx2-vnni", "ref"):
+            i = ol.ref_index(bid)
+            if i >= 0 and ol.ref().pkref_usable(i):
+                impls.append(("reference", bid, i))
+    if not impls:
+        impls.append(("port", "oracle", -1))
+    results = {}
+    for kind, bid, idx in impls[:1] + [x for x in impls[1:] if x[1] == "ref"]:
+        bufs = []
+        for (x, w, ws, M, K, N, add) in prods_host:
+            q = np.zeros(M * K, np.int8)
+            d = np.zeros(M, np.float32)
+            out = np.zeros(M * N, np.float32)
+            bufs.append((x, w, ws, M, K, N, add, q, d, out))
+        lim = seconds if bid != "ref" else seconds / 2
+        # the scalar ref takes ~1.5 s a layer on 16 cores: a quarter of the layer's frames
+        frac = 1.0 if bid != "ref" else 0.25
+        reps, ops, t0 = 0, 0.0, time.perf_counter()
+        while True:
+            for (x, w, ws, M, K, N, add, q, d, out) in bufs:
+                Ms = max(1, int(M * frac))
+                a = ol.Act(q.ctypes.data, d.ctypes.data, K, K, Ms)
+                if idx >= 0:
+                    ol.ref().pkref_quantize_threads(idx, cores, ctypes.byref(a), x.ctypes.data, K)
+                    ol.ref().pkref_gemm_threads(idx, cores, out.ctypes.data, N, w.ctypes.data, ws.ctypes.data,
+                                                None, N, ctypes.byref(a), add)
+                else:
+                    o = ol.oracle()
+                    fq = ctypes.cast(o.pko_quantize, ctypes.c_void_p).value
+                    fg = ctypes.cast(o.pko_gemm_q8, ctypes.c_void_p).value
+                    o.pko_quantize_threads(fq, cores, ctypes.byref(a), x.ctypes.data, K)
+                    o.pko_gemm_threads(fg, cores, out.ctypes.data, N, w.ctypes.data, ws.ctypes.data, None, N,
+                                       ctypes.byref(a), add)
+                ops += 2.0 * Ms * K * N
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= lim:
+                break
+        results[bid] = dict(kind=kind, tops=ops / el / 1e12, reps=reps, seconds=el, cores=cores, frac=frac)
+    return results
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ------------------------------------------------------------------ main ---
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run "
+              "(the int8 path would shard frames across GPUs with no exchange, DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import libpktito_amd as pk
+    pk.init()
+    torch.cuda.set_device(0)
+
+    M = 750
+    prods = make_layer(pk, torch, M, seed=1)
+    step = layer_step(pk, prods)
+    graph = graph_of(torch, step)
+    if args.profile_kernel:
+        dom = next(p for p in prods if p.name == args.profile_kernel)
+        for _ in range(50):
+            dom.gemm(pk)
+        torch.cuda.synchronize()
+        print(json.dumps({"profiled": dom.name, "kernel": pk.last_kernel()}))
+        return
+    log("layer M=750 captured")
+    replay_ok = check_replay(pk, torch, prods, graph)
+    ms = time_graph(torch, graph, args.steps, args.warmup)
+    ops = sum(p.ops() for p in prods)
+    tops = ops / (ms * 1e-3) / 1e12
+
+    # the dominant kernel: the product whose kernel takes the most time a step
+    per = []
+    for p in prods:
+        kms = kernel_ms(pk, torch, p)
+        per.append((kms, p, pk.last_kernel()))
+    per.sort(key=lambda t: -t[0])
+    dkms, dom, dname = per[0]
+    dbytes = dom.gemm_bytes()
+    intensity = dom.ops() / dbytes
+    achieved = dbytes / (dkms * 1e-3) / 1e9
+    bound = "hbm" if intensity < MFMA_INT8_PEAK_TOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
+    roofline = dict(bound=bound, kernel=dname, product=f"{dom.name} M={dom.M} K={dom.K} N={dom.N}",
+                    unit="GB/s" if bound == "hbm" else "TFLOP/s",
+                    achieved=round(achieved if bound == "hbm" else dom.ops() / (dkms * 1e-3) / 1e12, 1),
+                    peak=HBM_PEAK_GBS if bound == "hbm" else MFMA_INT8_PEAK_TOPS,
+                    kernel_us=round(dkms * 1e3, 3), bytes_per_launch=dbytes, ops_per_launch=dom.ops(),
+                    traffic=None)
+    roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
+    per_product = {p.name: dict(us=round(k * 1e3, 2), kernel=n,
+                                tops=round(p.ops() / (k * 1e-3) / 1e12, 1),
+                                GBs=round(p.gemm_bytes() / (k * 1e-3) / 1e9, 1)) for (k, p, n) in per}
+
+    extra = dict(pct_mfma_peak=round(100 * tops / MFMA_INT8_PEAK_TOPS, 2), per_product=per_product,
+                 graph_replay_matches_eager=replay_ok,
+                 layer_quantize_bytes=sum(p.quant_bytes() for p in prods),
+                 layer_gemm_bytes=sum(p.gemm_bytes() for p in prods))
+
+    cpu = None
+    host_inputs = [(p.x_host.reshape(-1), p.w, p.ws, p.M, p.K, p.N, p.add) for p in prods]
+    log(f"layer: {ms:.4f} ms a step, {tops:.1f} TOPS; dominant {dom.name} {dkms * 1e3:.2f} us")
+    if not args.quick:
+        # the long-form layer, M = 7500 (one segment of ten minutes)
+        long_prods = make_layer(pk, torch, 7500, seed=2)
+        gl = graph_of(torch, layer_step(pk, long_prods))
+        lms = time_graph(torch, gl, 10, 3)
+        lops = sum(p.ops() for p in long_prods)
+        long_per = {}
+        for p in long_prods:
+            kms = kernel_ms(pk, torch, p, launches=8, reps=2)
+            long_per[p.name] = dict(us=round(kms * 1e3, 1), tops=round(p.ops() / (kms * 1e-3) / 1e12, 1),
+                                    pct_mfma=round(100 * p.ops() / (kms * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS, 1),
+                                    kernel=pk.last_kernel())
+        log(f"long form: {lms:.3f} ms a layer")
+        extra["long_form_M7500"] = dict(ms_per_layer=round(lms, 4), tops=round(lops / (lms * 1e-3) / 1e12, 1),
+                                        pct_mfma_peak=round(100 * lops / (lms * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS, 1),
+                                        per_product=long_per)
+        for p in long_prods:
+            p.m.release()
+        del long_prods, gl
+        torch.cuda.empty_cache()
+
+        # a ragged batch of 8 segments (12-60 s), each product one
+        # grouped launch over the segments (the quantize over their rows at once)
+        from libpktito_amd import synth
+        lens = synth.ragged_lengths()
+        rg = synth.rng(3)
+        dev = torch.device("cuda")
+        rag = []
+        tot = sum(lens)
+        offs = np.cumsum([0] + lens)
+        for (name, mm, K, N, half, add) in synth.layer_products(750):
+            if name == "pos":
+                continue    # the positions' rows are per segment (2M - 1), not a frame batch
+            p = Product(pk, torch, name, tot, K, N, half, add, rg)
+            segs = [(p.out[offs[i]:offs[i + 1]], N, p.q[offs[i]:offs[i + 1]], p.d[offs[i]:offs[i + 1]],
+                     K, K, lens[i]) for i in range(len(lens))]
+            rag.append((p, segs))
+
+        def rag_step():
+            for p, segs in rag:
+                p.quantize(pk)
+                pk.gemm_q8_grouped_dev(p.m, 0, p.N, p.m.dev_scales, None, segs, p.add)
+        grg = graph_of(torch, rag_step)
+        rms = time_graph(torch, grg, 20, 3)
+        rops = sum(p.ops() for p, _ in rag)
+        log(f"ragged: {rms:.3f} ms")
+        extra["ragged_8_segments"] = dict(frames=lens, ms_per_layer_ex_pos=round(rms, 4),
+                                          tops=round(rops / (rms * 1e-3) / 1e12, 1))
+        for p, _ in rag:
+            p.m.release()
+        del rag, grg
+
+        # the 24-layer chained sweep, ms of encoder products per audio-minute
+        sweep = {}
+        for Ms in (750, 7500):
+            fn, sops, layers = encoder_sweep(pk, torch, Ms, seed=10 + Ms)
+            gs = graph_of(torch, fn)
+            sms = time_graph(torch, gs, 5 if Ms == 750 else 2, 1)
+            minutes = Ms / 750.0
+            log(f"encoder sweep M={Ms}: {sms:.3f} ms")
+            sweep[f"M{Ms}"] = dict(ms_total=round(sms, 3), ms_per_audio_minute=round(sms / minutes, 4),
+                                   tops=round(sops / (sms * 1e-3) / 1e12, 1),
+                                   weights_MB=round(sum(p.N * p.K for lay in layers for p in lay.values()) / 1e6, 1))
+            for lay in layers:
+                for p in lay.values():
+                    p.m.release()
+            del layers, gs, fn
+            torch.cuda.empty_cache()
+        extra["encoder_24_layers"] = sweep
+
+        # skinny shapes against HBM
+        extra["skinny"] = skinny_rates(pk, torch, [(1024, 4096, 4096), (4096, 1024, 1024), (640, 1040, 1030)])
+
+        log("skinny done")
+        if not args.no_cpu:
+            cpu = cpu_baseline(host_inputs, args.cpu_seconds)
+            log("cpu baseline done")
+
+    line = {
+        "metric": "int8 GEMM TOPS (% of MFMA peak); encoder-GEMM ms per audio-minute, 1 GPU",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded int8 weights, fp32 N(0,1) inputs; random-init weights of the layer's shapes)",
+        "config": {"workload": "FastConformer layer int8 products at M=750 (1 min audio): q,k,v,o,pos(2M-1),"
+                               "ff1/ff2 up 1024->4096 and down 4096->1024, pw1 1024->2048, pw2; "
+                               "per-row quantize + gemm_q8 each, one HIP graph a step",
+                   "M": M, "d_model": 1024, "ff": 4096, "qb": "per-row (n)", "products": len(prods),
+                   "ops_per_step": ops},
+        "roofline": roofline,
+        "cpu_baseline": None,
+        "extra": extra,
+    }
+    if cpu:
+        first = next(iter(cpu.values()))
+        name = next(iter(cpu))
+        line["cpu_baseline"] = dict(value=round(first["tops"], 4), unit="TOPS", cores=first["cores"],
+                                    kind=first["kind"],
+                                    sample=f"the same layer's 11 products (quantize + gemm_q8, M=750) on "
+                                           f"{name}, {first['reps']} passes in {first['seconds']:.1f} s, "
+                                           f"{first['cores']} threads, {cpu_model()}")
+        if "ref" in cpu and name != "ref":
+            r = cpu["ref"]
+            line["extra"]["cpu_ref_scalar"] = dict(tops=round(r["tops"], 5), cores=r["cores"], kind=r["kind"],
+                                                   sample=f"ref scalar on {int(r['frac'] * 100)}% of the frames, "
+                                                          f"{r['reps']} passes in {r['seconds']:.1f} s")
+    for p in prods:
+        p.m.release()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

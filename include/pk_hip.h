@@ -140,9 +140,17 @@ int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, c
                                const float *bias, const pk_hip_seg *segs, uint32_t nseg, int add,
                                void *stream);
 
-/* Statistics of the last device product launched on this thread: the kernel
- * variant's name, for profiling and tests. */
+/* The kernel variant the calling thread launched last, for profiling and
+ * tests. */
 const char *pk_hip_last_kernel(void);
+
+/* Tests and tuning: the number of tilings of the per-column product, and
+ * forcing one of them for every later launch in the process (-1 restores
+ * the automatic choice); returns the index forced before. Not thread-safe
+ * against launches in flight on other threads. Every tiling computes the
+ * same bits. */
+int pk_hip_tilings(void);
+int pk_hip_force_tiling(int index);
 
 #ifdef __cplusplus
 }

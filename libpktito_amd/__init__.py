@@ -57,6 +57,8 @@ _SIGS = {
     "pk_hip_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "pk_hip_last_error": (ctypes.c_char_p, []),
     "pk_hip_last_kernel": (ctypes.c_char_p, []),
+    "pk_hip_tilings": (ctypes.c_int, []),
+    "pk_hip_force_tiling": (ctypes.c_int, [ctypes.c_int]),
     "pk_hip_init": (ctypes.c_int, []),
     "pk_hip_upload_q8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32]),
     "pk_hip_release_q8": (ctypes.c_int, [ctypes.c_void_p]),
@@ -115,6 +117,17 @@ def init():
 def last_kernel():
     """The kernel variant the calling thread launched last."""
     return lib().pk_hip_last_kernel().decode()
+
+
+def tilings():
+    """How many tilings the per-column product has (pk_hip_tilings)."""
+    return lib().pk_hip_tilings()
+
+
+def force_tiling(index):
+    """Force tiling `index` for every later launch (-1: automatic); returns
+    the one forced before."""
+    return lib().pk_hip_force_tiling(index)
 
 
 def _ptr(a):

@@ -220,12 +220,14 @@ int launch_product(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint3
                    const float *ws, const float *bias, const pk_hip_act *a, int add, int rmode,
                    hipStream_t s) {
     pkq8::GemmArgs g;
-    g.w = m->w + (size_t)(r0 / 16) * m->ku * pkq8::kUnitBytes;
+    g.w = m->w + (size_t)(r0 / 16) * pkq8::kUnitBytes;
+    g.wstride = (uint64_t)(m->rows / 16) * pkq8::kUnitBytes;
     g.ws = ws;
     g.bias = bias;
     g.rows = rows;
     g.n = a->n;
     g.ku = m->ku;
+    g.kr = pkq8::units_with_data(m->cols);
     g.qb = a->qb;
     g.nb = a->n / a->qb;
     g.add = add;
@@ -272,6 +274,10 @@ const char *pk_hip_strerror(int err) {
 const char *pk_hip_last_error(void) { return g_err; }
 
 const char *pk_hip_last_kernel(void) { return g_kernel; }
+
+int pk_hip_tilings(void) { return pkq8::ring_count(); }
+
+int pk_hip_force_tiling(int index) { return pkq8::set_ring(index); }
 
 int pk_hip_init(void) {
     std::call_once(g_once, init_once);
@@ -524,12 +530,14 @@ int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, c
     if ((e = check_panel(m, r0, rows, n)))
         return e;
     pkq8::GemmArgs g;
-    g.w = m->w + (size_t)(r0 / 16) * m->ku * pkq8::kUnitBytes;
+    g.w = m->w + (size_t)(r0 / 16) * pkq8::kUnitBytes;
+    g.wstride = (uint64_t)(m->rows / 16) * pkq8::kUnitBytes;
     g.ws = ws;
     g.bias = bias;
     g.rows = rows;
     g.n = n;
     g.ku = m->ku;
+    g.kr = pkq8::units_with_data(m->cols);
     g.qb = qb;
     g.nb = n / qb;
     g.add = add;

@@ -12,13 +12,19 @@ namespace pkq8 {
 /* A matrix in HBM, repacked from PK_Q8 (16-row panels, groups of 4 inputs)
  * into units of 16 rows by 64 inputs: a unit is 1 KB, the 16 rows' 64 bytes
  * in the order the 16x16x64 int8 MFMA takes an operand (byte 16 * (kq * 16 +
- * r) + kb holds row r, input 16 * kq + kb of the unit), and a panel's ku =
- * ceil(cols / 64) units follow one another, inputs past cols zero. A panel
- * is therefore 1 KB * ku contiguous bytes, and any whole panel of the matrix
- * starts a valid matrix of fewer rows. */
+ * r) + kb holds row r, input 16 * kq + kb of the unit). Units are stored
+ * stage-major: unit u of every panel, then unit u + 1 of every panel, so
+ * unit (p, u) is at 1 KB * (u * panels + p) and the workgroups that load one
+ * stage at once read one contiguous run of memory (a panel-major layout puts
+ * a stage's units a panel's length apart, onto few HBM channels). Each panel
+ * has ku units, ceil(cols / 64) rounded up to a multiple of 4 so that the
+ * pipelined product's four-slot ring divides it, inputs past cols zero. A
+ * run of panels starting at panel p0 is the matrix at byte 1 KB * p0 with the
+ * same unit stride. */
 constexpr uint32_t kUnitBytes = 1024;
 
-inline uint32_t units_per_panel(uint32_t cols) { return (cols + 63) / 64; }
+inline uint32_t units_with_data(uint32_t cols) { return (cols + 63) / 64; }
+inline uint32_t units_per_panel(uint32_t cols) { return (units_with_data(cols) + 3) & ~3u; }
 
 /* One segment of activations and outputs. */
 struct Seg {
@@ -39,11 +45,13 @@ struct SegTable {
 
 /* What every product launch shares. */
 struct GemmArgs {
-    const int8_t *w;            /* repacked weights, at the first panel of the call */
+    const int8_t *w;            /* repacked weights: unit 0 of the call's first panel */
+    uint64_t wstride;           /* bytes from a panel's unit u to its unit u + 1 */
     const float *ws, *bias;     /* at the first row of the call */
     uint32_t rows;              /* N, a multiple of 16 */
     uint32_t n;                 /* K, a multiple of 32 */
-    uint32_t ku;                /* units a panel */
+    uint32_t ku;                /* units a panel (the stride, a multiple of 4) */
+    uint32_t kr;                /* units holding inputs: ceil(n / 64) */
     uint32_t qb, nb;            /* block inputs, blocks a column */
     int add;
     int rmode;                  /* 0 nearest, 1 upward, 2 downward, 3 toward zero */
@@ -53,6 +61,11 @@ int launch_repack(int8_t *dst, const int8_t *src, uint32_t rows, uint32_t cols, 
 
 int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb,
                     uint32_t T, hipStream_t s, const char **name);
+
+/* The pipelined product's tilings: how many, and forcing one (-1: the
+ * heuristic); returns the one forced before. */
+int ring_count();
+int set_ring(int i);
 
 /* One product; table->nseg == 1 for a plain call. */
 int launch_gemm(const GemmArgs &g, const SegTable &table, hipStream_t s, const char **name);

@@ -15,6 +15,8 @@
 #include <float.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #pragma clang fp contract(off)
 
 namespace pkq8 {
@@ -185,17 +187,63 @@ __global__ __launch_bounds__(256) void quant_any_kernel(int8_t *__restrict__ q, 
     d[i] = dv;
 }
 
+/* A whole column is one block, n <= 4096: one wave a column, four columns a
+ * workgroup, each lane CH float4 chunks of it (chunk c of lane l is float4
+ * l + 64 c), every load issued before the first is used. */
+template <int CH>
+__global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q, float *__restrict__ d,
+                                                         const float *__restrict__ x, size_t xs,
+                                                         uint32_t n, uint32_t T) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T)
+        return;
+    const uint32_t n4 = n >> 2;
+    const float4 *xr = (const float4 *)(x + (size_t)t * xs);
+    float4 v[CH];
+    float amax = 0.0f;
+    int nan = 0;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        v[c] = i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+        absmax4(v[c], amax, nan);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        nan |= __shfl_xor(nan, off, 64);
+    }
+    const bool zero = zero_block(amax, nan);
+    float dv = 0.0f, id = 0.0f;
+    if (!zero) {
+        dv = amax / 127.0f;
+        id = 127.0f / amax;
+    }
+    int *qr = (int *)(q + (size_t)t * n);
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < n4)
+            qr[i] = zero ? 0 : pack4(v[c], id);
+    }
+    if (lane == 0)
+        d[t] = dv;
+}
+
 int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb,
                     uint32_t T, hipStream_t s, const char **name) {
     if (T == 0)
         return 0;
-    const uint32_t nch = n / 16;
-    if (qb == n && nch <= 64) {
-        quant_col_kernel<1, 1><<<T, 64, 0, s>>>(q, d, x, xs, n);
-        *name = "quant_col<1,1>";
-    } else if (qb == n && nch <= 256) {
-        quant_col_kernel<4, 1><<<T, 256, 0, s>>>(q, d, x, xs, n);
-        *name = "quant_col<4,1>";
+    const uint32_t nch = n / 16, n4 = n / 4, grid4 = (T + 3) / 4;
+    if (qb == n && n4 <= 256) {
+        quant_wave_kernel<4><<<grid4, 256, 0, s>>>(q, d, x, xs, n, T);
+        *name = "quant_wave<4>";
+    } else if (qb == n && n4 <= 1024) {
+        quant_wave_kernel<16><<<grid4, 256, 0, s>>>(q, d, x, xs, n, T);
+        *name = "quant_wave<16>";
     } else if (qb == n && nch <= 1024) {
         quant_col_kernel<4, 4><<<T, 256, 0, s>>>(q, d, x, xs, n);
         *name = "quant_col<4,4>";
@@ -224,7 +272,9 @@ int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, 
 /* -------------------------------------------------------------- repack --
  *
  * PK_Q8 (core/pkf.h:28-41: q(r, k) at ((r/16)(cols/4) + k/4) 64 + (r%16) 4 +
- * k%4) into units (q8_internal.h): one thread a 16-byte lane slot. */
+ * k%4) into units (q8_internal.h), stage-major: unit (p, u) of panel p and
+ * inputs [64 u, 64 u + 64) at byte 1024 (u panels + p). One thread a 16-byte
+ * lane slot. */
 __global__ __launch_bounds__(256) void repack_kernel(int8_t *__restrict__ dst,
                                                      const int8_t *__restrict__ src,
                                                      uint32_t panels, uint32_t cols, uint32_t ku) {
@@ -232,8 +282,8 @@ __global__ __launch_bounds__(256) void repack_kernel(int8_t *__restrict__ dst,
     if (slot >= (uint64_t)panels * ku * 64)
         return;
     const uint32_t lane = (uint32_t)(slot & 63);
-    const uint64_t unit = slot >> 6;
-    const uint32_t p = (uint32_t)(unit / ku), u = (uint32_t)(unit % ku);
+    const uint64_t unit = slot >> 6;                 /* u * panels + p */
+    const uint32_t u = (uint32_t)(unit / panels), p = (uint32_t)(unit % panels);
     const uint32_t r = lane & 15, kq = lane >> 4;
     const uint32_t k0 = u * 64 + kq * 16;
     int o[4];
@@ -300,7 +350,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const Seg &sg, uint
     const uint32_t T = sg.T;
     const uint32_t n0 = tn * BN, m0 = tm * BM;
     const uint32_t npan = g.rows >> 4;
-    const uint32_t n = g.n, ku = g.ku;
+    const uint32_t n = g.n, ku = g.ku, kr = g.kr;
 
     if (g.rmode)
         __builtin_amdgcn_s_setreg(2049, g.rmode);    /* MODE.FP_ROUND, single precision */
@@ -315,7 +365,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const Seg &sg, uint
         if (u < UB) {
             uint32_t p = n0 / 16 + u;
             p = p < npan ? p : npan - 1;
-            src[s] = g.w + (size_t)p * ku * kUnitBytes + lane * 16;
+            src[s] = g.w + (size_t)p * kUnitBytes + lane * 16;
             isw[s] = true;
         } else {
             uint32_t row = m0 + (u - UB) * 16 + (lane & 15);
@@ -330,7 +380,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const Seg &sg, uint
 #pragma unroll
         for (int s = 0; s < LPW; s++) {
             if (isw[s]) {
-                stage[s] = *(const v4i *)(src[s] + (size_t)kt * kUnitBytes);
+                stage[s] = *(const v4i *)(src[s] + (size_t)kt * g.wstride);
             } else {
                 /* inputs past n: the row's first 16, against zero weights */
                 const uint32_t k = kt * 64 + (lane >> 4) * 16;
@@ -389,9 +439,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const Seg &sg, uint
     gload(0);
     lstore(0);
     __syncthreads();
-    for (uint32_t kt = 0; kt < ku; kt++) {
+    for (uint32_t kt = 0; kt < kr; kt++) {
         const int cur = kt & 1;
-        if (kt + 1 < ku)
+        if (kt + 1 < kr)
             gload(kt + 1);
         const int8_t *lb = &lds[cur][0];
         if (MODE != 2) {
@@ -435,7 +485,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const Seg &sg, uint
                     chain(kend / g.qb - 1);
             }
         }
-        if (kt + 1 < ku)
+        if (kt + 1 < kr)
             lstore(cur ^ 1);
         __syncthreads();
     }
@@ -509,26 +559,27 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_q8_grouped_kernel(GemmArgs 
 template <int KW>
 __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg sg) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t p = blockIdx.x, n = g.n, ku = g.ku, T = sg.T;
+    const uint32_t p = blockIdx.x, n = g.n, ku = g.ku, kr = g.kr, T = sg.T;
     if (g.rmode)
         __builtin_amdgcn_s_setreg(2049, g.rmode);
-    const int8_t *wp = g.w + (size_t)p * ku * kUnitBytes + lane * 16;
+    const int8_t *wp = g.w + (size_t)p * kUnitBytes + lane * 16;
+    const size_t ws_ = g.wstride;
     uint32_t row = lane & 15;
     row = row < T ? row : T - 1;
     const int8_t *ap = sg.q + (size_t)row * n;
     v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
     uint32_t u = wave;
-    for (; u + KW < ku; u += 2 * KW) {
-        const v4i w0 = *(const v4i *)(wp + (size_t)u * kUnitBytes);
-        const v4i w1 = *(const v4i *)(wp + (size_t)(u + KW) * kUnitBytes);
+    for (; u + KW < kr; u += 2 * KW) {
+        const v4i w0 = *(const v4i *)(wp + (size_t)u * ws_);
+        const v4i w1 = *(const v4i *)(wp + (size_t)(u + KW) * ws_);
         const uint32_t k0 = u * 64 + (lane >> 4) * 16, k1 = k0 + KW * 64;
         const v4i a0 = *(const v4i *)(ap + (k0 < n ? k0 : 0));
         const v4i a1 = *(const v4i *)(ap + (k1 < n ? k1 : 0));
         acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0, a0, acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w1, a1, acc1, 0, 0, 0);
     }
-    if (u < ku) {
-        const v4i w0 = *(const v4i *)(wp + (size_t)u * kUnitBytes);
+    if (u < kr) {
+        const v4i w0 = *(const v4i *)(wp + (size_t)u * ws_);
         const uint32_t k0 = u * 64 + (lane >> 4) * 16;
         const v4i a0 = *(const v4i *)(ap + (k0 < n ? k0 : 0));
         acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0, a0, acc0, 0, 0, 0);
@@ -555,6 +606,346 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
             v = v + g.bias[c + r];
         o[r] = g.add ? o[r] + v : v;
     }
+}
+
+/* ----------------------------------------------- the pipelined product --
+ *
+ * MODE 0 (a block a column) with its loads in flight several stages ahead:
+ * each stage's units go straight from global memory into LDS
+ * (global_load_lds_dwordx4: a wave's 64 lanes write 1 KB, lane l at byte
+ * 16 l, which is the unit layout), into a ring of four slots. At stage kt
+ * a thread waits until its own loads of stage kt have landed (vmcnt counts
+ * its later stages still in flight), the workgroup meets at a barrier, the
+ * loads of stage kt + 3 go into the slot stage kt - 1 used, and the MFMAs
+ * run on slot kt. Three stages are in flight while one is multiplied. The
+ * slots are four distinct LDS arrays and the loop is unrolled by four, so
+ * the compiler sees which slot each read and each load touches. */
+
+#define PK_AS1(p) ((const void __attribute__((address_space(1))) *)(p))
+#define PK_AS3(p) ((void __attribute__((address_space(3))) *)(p))
+
+/* s_waitcnt vmcnt(N), expcnt and lgkmcnt left alone (gfx9 encoding) */
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+/* the LDS byte address of a __shared__ pointer */
+__device__ __forceinline__ uint32_t lds_addr(const int8_t *p) {
+    return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) int8_t *)p);
+}
+
+/* 16 bytes from LDS, issued as written; the caller waits on lgkmcnt */
+__device__ __forceinline__ v4i lds_read16(uint32_t addr) {
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+    return r;
+}
+
+/* f(integral_constant<int, I>) for I in [I0, N), unrolled at compile time */
+template <int I, int N, typename F>
+__device__ __forceinline__ void for_static(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        for_static<I + 1, N>(f);
+    }
+}
+
+/* s_waitcnt lgkmcnt(N), the other counters untouched */
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt is four bits");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+
+/* A stage is UPS units of inputs (64 UPS of K) for the tile's UB weight
+ * panels and UA frame groups: slot layout [kk < UPS][unit < UA + UB], 1 KB a
+ * unit. Within a stage the fragments of sub-step kk + 1 are read while the
+ * MFMAs of sub-step kk run (two register sets). */
+template <int WN, int WM, int TN, int TM, int UPS>
+__device__ __forceinline__ void ring_tile(const GemmArgs &g, const Seg &sg, uint32_t tn, uint32_t tm) {
+    constexpr int NW = WN * WM;
+    constexpr int BN = 16 * TN * WN, BM = 16 * TM * WM;
+    constexpr int UB = BN / 16, UA = BM / 16, UNITS = UA + UB;
+    constexpr int SLOTU = UNITS * UPS;
+    static_assert(SLOTU % NW == 0, "each wave loads whole units");
+    constexpr int L = SLOTU / NW;
+    static_assert(2 * L < 64, "the stages in flight fit vmcnt");
+    constexpr int SLOT = SLOTU * kUnitBytes;
+    static_assert(4 * SLOT <= 160 * 1024, "four slots fit a CU's LDS");
+    constexpr int R = TN + TM;
+    __shared__ __attribute__((aligned(1024))) int8_t s0[SLOT], s1[SLOT], s2[SLOT], s3[SLOT];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   /* uniform: scalar */
+    const int wn = wave % WN, wm = wave / WN;
+    const uint32_t T = sg.T;
+    const uint32_t n0 = tn * BN, m0 = tm * BM;
+    const uint32_t npan = g.rows >> 4;
+    const uint32_t n = g.n, ku = g.ku, ns = g.ku / UPS;
+
+    if (g.rmode)
+        __builtin_amdgcn_s_setreg(2049, g.rmode);    /* MODE.FP_ROUND, single precision */
+
+    /* this thread's lane of slot units [wave L, wave L + L): sub-step kk,
+     * unit u (weights first) */
+    const int8_t *src[L];
+    bool isw[L];
+    uint32_t sub[L];
+#pragma unroll
+    for (int s = 0; s < L; s++) {
+        const int idx = wave * L + s, kk = idx / UNITS, u = idx % UNITS;
+        sub[s] = kk;
+        if (u < UB) {
+            uint32_t p = n0 / 16 + u;
+            p = p < npan ? p : npan - 1;
+            src[s] = g.w + (size_t)p * kUnitBytes + lane * 16;
+            isw[s] = true;
+        } else {
+            uint32_t row = m0 + (u - UB) * 16 + (lane & 15);
+            row = row < T ? row : T - 1;
+            src[s] = sg.q + (size_t)row * n;
+            isw[s] = false;
+        }
+    }
+    auto issue = [&](uint32_t j, int8_t *slot) {
+#pragma unroll
+        for (int s = 0; s < L; s++) {
+            const uint32_t unit = j * UPS + sub[s];
+            const int8_t *gp;
+            if (isw[s]) {
+                gp = src[s] + (size_t)unit * g.wstride;
+            } else {
+                /* inputs past n: the row's first 16, against zero weights */
+                const uint32_t k = unit * 64 + (lane >> 4) * 16;
+                gp = src[s] + (k < n ? k : 0);
+            }
+            __builtin_amdgcn_global_load_lds(PK_AS1(gp), PK_AS3(slot + (wave * L + s) * kUnitBytes), 16, 0, 0);
+        }
+    };
+
+    v4i acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; i++)
+#pragma unroll
+        for (int j = 0; j < TM; j++)
+            acc[i][j] = v4i{0, 0, 0, 0};
+
+    /* The fragments are read with ds_read_b128 written out, and waited for
+     * with lgkmcnt before the MFMAs take them: the compiler, which cannot
+     * tell the ring's slots apart across the loop's back edge, would
+     * otherwise wait for every load in flight before the first read of each
+     * pass. The barrier in landed() orders these reads after the loads. */
+    const uint32_t wbase = lds_addr(s0) + (wn * TN) * kUnitBytes + lane * 16;
+    const uint32_t abase = lds_addr(s0) + (UB + wm * TM) * kUnitBytes + lane * 16;
+    /* A sub-step's fragments are read activations first, then the weight
+     * fragments in order, and the MFMAs of weight fragment i start once it
+     * has landed (lgkmcnt counts the reads after it), so the LDS reads of a
+     * sub-step overlap its own MFMAs. */
+    v4i f[R];
+    auto sub_step = [&](uint32_t at) {
+#pragma unroll
+        for (int j = 0; j < TM; j++)
+            f[TN + j] = lds_read16(abase + at + j * kUnitBytes);
+#pragma unroll
+        for (int i = 0; i < TN; i++)
+            f[i] = lds_read16(wbase + at + i * kUnitBytes);
+        for_static<0, TN>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            wait_lgkm<(TN - 1 - i < 15 ? TN - 1 - i : 15)>();
+            asm volatile("" : "+v"(f[i]));
+            if (i == 0) {
+#pragma unroll
+                for (int j = 0; j < TM; j++)
+                    asm volatile("" : "+v"(f[TN + j]));
+            }
+#pragma unroll
+            for (int j = 0; j < TM; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f[i], f[TN + j], acc[i][j], 0, 0, 0);
+        });
+    };
+    auto compute = [&](const int8_t *lb) {
+        const uint32_t at = lds_addr(lb) - lds_addr(s0);
+#pragma unroll
+        for (int kk = 0; kk < UPS; kk++)
+            sub_step(at + kk * UNITS * kUnitBytes);
+    };
+    /* stage kt landed in every wave: at most min(2, ns - 1 - kt) later
+     * stages of this thread's loads still in flight, then the barrier */
+    auto landed = [&](uint32_t kt) {
+        const uint32_t later = ns - 1 - kt;
+        if (later >= 2)
+            wait_vm<2 * L>();
+        else if (later == 1)
+            wait_vm<L>();
+        else
+            wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+    };
+
+    /* ns is a multiple of four: every pass of the loop is four whole stages */
+    issue(0, s0);
+    issue(1, s1);
+    issue(2, s2);
+    for (uint32_t kt = 0; kt < ns; kt += 4) {
+        landed(kt);
+        if (kt + 3 < ns)
+            issue(kt + 3, s3);
+        compute(s0);
+        landed(kt + 1);
+        if (kt + 4 < ns)
+            issue(kt + 4, s0);
+        compute(s1);
+        landed(kt + 2);
+        if (kt + 5 < ns)
+            issue(kt + 5, s1);
+        compute(s2);
+        landed(kt + 3);
+        if (kt + 6 < ns)
+            issue(kt + 6, s2);
+        compute(s3);
+    }
+    wait_vm<0>();
+
+    /* the epilogue: ref's operations in ref's order, four channels a lane */
+    const bool vec = ((sg.os & 3) == 0) && ((((uintptr_t)sg.out) & 15) == 0);
+#pragma unroll
+    for (int j = 0; j < TM; j++) {
+        const uint32_t t = m0 + (wm * TM + j) * 16 + (lane & 15);
+        if (t >= T)
+            continue;
+        const float dt = sg.d[t];
+#pragma unroll
+        for (int i = 0; i < TN; i++) {
+            const uint32_t c = n0 + (wn * TN + i) * 16 + (lane >> 4) * 4;
+            if (c >= g.rows)
+                continue;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                v[r] = __builtin_fmaf((float)acc[i][j][r], dt, 0.0f) * g.ws[c + r];
+                if (g.bias)
+                    v[r] = v[r] + g.bias[c + r];
+            }
+            float *o = sg.out + (size_t)t * sg.os + c;
+            if (vec) {
+                float4 ov = make_float4(v[0], v[1], v[2], v[3]);
+                if (g.add) {
+                    const float4 old = *(const float4 *)o;
+                    ov.x = old.x + ov.x;
+                    ov.y = old.y + ov.y;
+                    ov.z = old.z + ov.z;
+                    ov.w = old.w + ov.w;
+                }
+                *(float4 *)o = ov;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    o[r] = g.add ? o[r] + v[r] : v[r];
+            }
+        }
+    }
+}
+
+/* The hardware deals workgroup b to XCD b % 8. Renumbered so that each XCD
+ * takes a contiguous run of tiles, and the run ordered in groups of 8 frame
+ * tiles by every channel tile, the workgroups one XCD runs at once share
+ * their inputs and weights in its L2. */
+__device__ __forceinline__ void xcd_tile(uint32_t b, uint32_t nwg, uint32_t tiles_n, uint32_t tiles_m,
+                                         uint32_t &tn, uint32_t &tm) {
+    const uint32_t per = nwg / 8, rem = nwg % 8, x = b % 8, i = b / 8;
+    const uint32_t nb = x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+    constexpr uint32_t GM = 8;
+    const uint32_t group = nb / (GM * tiles_n), idx = nb % (GM * tiles_n);
+    const uint32_t first = group * GM;
+    const uint32_t gm = tiles_m - first < GM ? tiles_m - first : GM;
+    tm = first + idx % gm;
+    tn = idx / gm;
+}
+
+template <int WN, int WM, int TN, int TM, int UPS>
+__global__ __launch_bounds__(64 * WN * WM) void gemm_ring_kernel(GemmArgs g, Seg sg, uint32_t tiles_n,
+                                                                 uint32_t tiles_m) {
+    uint32_t tn, tm;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_n, tiles_m, tn, tm);
+    ring_tile<WN, WM, TN, TM, UPS>(g, sg, tn, tm);
+}
+
+template <int WN, int WM, int TN, int TM, int UPS>
+__global__ __launch_bounds__(64 * WN * WM) void gemm_ring_grouped_kernel(GemmArgs g, SegTable tab,
+                                                                         uint32_t tiles_n) {
+    const uint32_t tm = blockIdx.x / tiles_n;
+    uint32_t i = 0;
+    while (i + 1 < tab.nseg && tab.s[i + 1].tile0 <= tm)
+        i++;
+    ring_tile<WN, WM, TN, TM, UPS>(g, tab.s[i], blockIdx.x % tiles_n, tm - tab.s[i].tile0);
+}
+
+template <int WN, int WM, int TN, int TM, int UPS>
+static void run_ring(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
+    constexpr uint32_t BN = 16 * TN * WN, BM = 16 * TM * WM;
+    const uint32_t tiles_n = (g.rows + BN - 1) / BN;
+    if (tab.nseg == 1) {
+        const uint32_t tiles_m = (tab.s[0].T + BM - 1) / BM;
+        gemm_ring_kernel<WN, WM, TN, TM, UPS><<<tiles_n * tiles_m, 64 * WN * WM, 0, s>>>(g, tab.s[0], tiles_n, tiles_m);
+    } else {
+        SegTable t = tab;
+        uint32_t tiles = 0;
+        for (uint32_t i = 0; i < t.nseg; i++) {
+            t.s[i].tile0 = tiles;
+            tiles += (t.s[i].T + BM - 1) / BM;
+        }
+        gemm_ring_grouped_kernel<WN, WM, TN, TM, UPS><<<tiles_n * tiles, 64 * WN * WM, 0, s>>>(g, t, tiles_n);
+    }
+}
+
+/* The pipelined product's tile shapes: channels x frames, and the units of
+ * inputs a stage (ku must divide into four stages of them). */
+struct RingCfg {
+    const char *name;
+    uint32_t bn, bm, ups;
+    void (*run)(const GemmArgs &, const SegTable &, hipStream_t);
+};
+static const RingCfg kRing[] = {
+    { "ring<128x128,1>", 128, 128, 1, run_ring<2, 2, 4, 4, 1> },
+    { "ring<128x128,2>", 128, 128, 2, run_ring<2, 2, 4, 4, 2> },
+    { "ring<64x64,1>", 64, 64, 1, run_ring<2, 2, 2, 2, 1> },
+    { "ring<64x64,2>", 64, 64, 2, run_ring<2, 2, 2, 2, 2> },
+    { "ring<64x64,4>", 64, 64, 4, run_ring<2, 2, 2, 2, 4> },
+    { "ring<128x64,2>", 128, 64, 2, run_ring<4, 1, 2, 4, 2> },
+    { "ring<256x128,1>", 256, 128, 1, run_ring<4, 2, 4, 4, 1> },
+    { "ring<128x256,1>", 128, 256, 1, run_ring<2, 4, 4, 4, 1> },
+    { "ring<64x128,2>", 64, 128, 2, run_ring<2, 2, 2, 4, 2> },
+    { "ring<256x256,1>", 256, 256, 1, run_ring<2, 2, 8, 8, 1> },
+    { "ring<256x256w8,1>", 256, 256, 1, run_ring<2, 4, 8, 4, 1> },
+    { "ring<256x128w4,1>", 256, 128, 1, run_ring<2, 2, 8, 4, 1> },
+    { "ring<128x256w4,1>", 128, 256, 1, run_ring<2, 2, 4, 8, 1> },
+};
+constexpr int kNRing = sizeof kRing / sizeof kRing[0];
+
+/* A forced tiling for tests and tuning (set_ring), -1 for the heuristic. */
+static int g_forced_ring = -1;
+
+int set_ring(int i) {
+    const int was = g_forced_ring;
+    g_forced_ring = i >= 0 && i < kNRing ? i : -1;
+    return was;
+}
+
+int ring_count() { return kNRing; }
+
+/* The tile for a product of `frames` frames into `rows` channels: the
+ * largest that still gives every CU a workgroup. */
+static int pick_ring(uint32_t rows, uint64_t frames, uint32_t ku) {
+    if (g_forced_ring >= 0 && ku % (4 * kRing[g_forced_ring].ups) == 0)
+        return g_forced_ring;
+    auto tiles = [&](int i) { return (uint64_t)((rows + kRing[i].bn - 1) / kRing[i].bn) * ((frames + kRing[i].bm - 1) / kRing[i].bm); };
+    if (tiles(0) >= 512)
+        return 0;
+    if (tiles(5) >= 256 && ku % 8 == 0)
+        return 5;
+    return ku % 16 == 0 ? 4 : ku % 8 == 0 ? 3 : 2;
 }
 
 template <int WN, int WM, int TN, int TM, int MODE>
@@ -606,6 +997,12 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
             gemm_q8_skinny_kernel<4><<<panels, 256, 0, s>>>(g, tab.s[0]);
             *name = "skinny<4>";
         }
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    if (mode == 0) {
+        const int c = pick_ring(g.rows, frames, g.ku);
+        kRing[c].run(g, tab, s);
+        *name = kRing[c].name;
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     /* 128 x 128 tiles where they fill the chip, 64 x 64 where they do not */

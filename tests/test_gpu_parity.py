@@ -251,3 +251,36 @@ def test_split_invariance_and_threads(hip):
             t.join()
     assert not errors, errors
     assert same(out, whole)
+
+
+def test_every_tiling(hip):
+    """Every tiling of the per-column product, forced, on shapes that leave
+    partial tiles in both directions, odd panel counts, K not a multiple of
+    64 and a run of panels from the middle; bit for bit against the oracle."""
+    shapes = [(750, 1024, 4096), (37, 96, 1040), (300, 640, 208), (129, 4096, 64), (1499, 1024, 1024), (17, 32, 16)]
+    try:
+        for ti in range(hip.tilings()):
+            hip.force_tiling(ti)
+            for (M, K, N) in shapes:
+                g = synth.rng(M + K + N)
+                w = synth.pack_q8(synth.weights(g, N, K))
+                ws = synth.scales(g, N)
+                bias = g.standard_normal(N).astype(np.float32)
+                x = synth.activations(g, M, K).reshape(-1)
+                q, d = ol.quantize(x, M, K, K, K)
+                r0 = 16 if N > 32 else 0
+                rows = N - r0
+                os_ = N + 4
+                base = g.standard_normal(M * os_).astype(np.float32)
+                for add in (0, 1):
+                    want, out = base.copy(), base.copy()
+                    ol.gemm_q8(want, os_, w, ws, bias, rows, q, d, K, K, M, add, r0=r0, threads=16)
+                    say("tiling", ti, M, K, N, add)
+                    with hip.Q8Matrix(w, ws):
+                        hip.gemm_q8(out, os_, w, ws[r0:], bias[r0:], rows, hip.make_act(q, d, K, K, M), add,
+                                    w_offset=r0 * K, out_offset=r0)
+                        if M > 16:
+                            assert hip.last_kernel().startswith("ring"), hip.last_kernel()
+                    assert same(out, want), (ti, M, K, N, add)
+    finally:
+        hip.force_tiling(-1)
