@@ -27,6 +27,7 @@ import json
 import os
 import sys
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -41,6 +42,10 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
+def _addr(a):
+    return a.ctypes.data
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -50,7 +55,10 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=8.0)
     p.add_argument("--profile-kernel", default=None,
-                   help="only launch the dominant kernel's timing loop (for rocprofv3 --pmc runs)")
+                   help="only launch the named product's kernel 50 times (for rocprofv3 --pmc runs)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only copy 256 MiB three times (the known-size kernel that scales "
+                        "rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -58,11 +66,13 @@ def parse():
 
 class Product:
     """One int8 product of the layer, resident in HBM: its uploaded matrix, its
-    fp32 input, and its quantized activations and fp32 output buffers."""
+    fp32 input, its quantized activations (row-major q, d, and the packed copy
+    the product reads) and its fp32 output."""
 
     def __init__(self, pk, torch, name, M, K, N, half, add, g, x_dev=None, xs=None, ws_gain=1.0):
         from libpktito_amd import synth
         self.name, self.M, self.K, self.N, self.add = name, M, K, N, int(add)
+        self.quantizes = True
         wr = synth.weights(g, N, K)
         self.w = synth.pack_q8(wr)
         self.ws = (synth.scales(g, N) * np.float32(ws_gain)).astype(np.float32)
@@ -77,7 +87,14 @@ class Product:
             self.x, self.xs = x_dev, xs
         self.q = torch.empty((M, K), dtype=torch.int8, device=dev)
         self.d = torch.empty((M,), dtype=torch.float32, device=dev)
+        self.qp = torch.empty((pk.packed_bytes(K, M),), dtype=torch.int8, device=dev)
         self.out = torch.zeros((M, N), dtype=torch.float32, device=dev)
+
+    def share(self, other):
+        """Take other's quantized activations as this product's input (the
+        reference multiplies q, k and v by one quantized activation)."""
+        self.quantizes = False
+        self.x_host, self.x, self.q, self.d, self.qp = other.x_host, other.x, other.q, other.d, other.qp
 
     def ops(self):
         return 2.0 * self.M * self.K * self.N
@@ -89,21 +106,39 @@ class Product:
     def quant_bytes(self):
         return 4 * self.M * self.K + self.M * self.K + 4 * self.M
 
-    def quantize(self, pk, stream=None):
-        pk.quantize_dev(self.q, self.d, self.x, self.K, self.K, self.M, self.xs, stream=stream)
+    def quantize(self, pk, stream=None, packed=True):
+        if packed:
+            # the products read the packed copy only: no row-major q is written
+            pk.quantize_packed_dev(None, self.qp, self.d, self.x, self.K, self.M, self.xs, stream=stream)
+        else:
+            pk.quantize_dev(self.q, self.d, self.x, self.K, self.K, self.M, self.xs, stream=stream)
 
-    def gemm(self, pk, stream=None):
-        pk.gemm_q8_dev(self.out, self.N, self.m, 0, self.N, None, None, self.q, self.d, self.K, self.K,
-                       self.M, self.add, ws_ptr=self.m.dev_scales, stream=stream)
+    def gemm(self, pk, stream=None, packed=True):
+        if packed:
+            pk.gemm_q8_packed_dev(self.out, self.N, self.m, 0, self.N, self.m.dev_scales, None, self.qp, self.d,
+                                  self.K, self.M, self.add, stream=stream)
+        else:
+            pk.gemm_q8_dev(self.out, self.N, self.m, 0, self.N, None, None, self.q, self.d, self.K, self.K,
+                           self.M, self.add, ws_ptr=self.m.dev_scales, stream=stream)
 
 
 def make_layer(pk, torch, M, seed, ws_gain=None):
+    """One layer's products in the reference's dataflow (core/encoder.c:329-368):
+    k and v multiply q's quantized activation; the positions' projection reads
+    positional encodings quantized once an encode (core/encoder.c:467-469), so
+    its quantize is done here, outside the layer step."""
     from libpktito_amd import synth
     g = synth.rng(seed)
     prods = []
     for (name, mm, K, N, half, add) in synth.layer_products(M):
         gain = 1.0 if ws_gain is None else ws_gain(K)
         prods.append(Product(pk, torch, name, mm, K, N, half, add, g, ws_gain=gain))
+    by = {p.name: p for p in prods}
+    by["k"].share(by["q"])
+    by["v"].share(by["q"])
+    by["pos"].quantize(pk)
+    by["pos"].quantizes = False
+    torch.cuda.synchronize()
     return prods
 
 
@@ -137,12 +172,12 @@ def time_graph(torch, g, reps, warmup):
     return e0.elapsed_time(e1) / reps
 
 
-def kernel_ms(pk, torch, prod, launches=64, reps=5):
+def kernel_ms(pk, torch, prod, launches=64, reps=5, packed=True):
     """The average duration of one product's kernel: a graph of `launches`
     back-to-back launches of it, timed with events on its stream."""
     def fn():
         for _ in range(launches):
-            prod.gemm(pk)
+            prod.gemm(pk, packed=packed)
     g = graph_of(torch, fn)
     best = min(time_graph(torch, g, 3, 1) for _ in range(reps))
     return best / launches
@@ -150,11 +185,12 @@ def kernel_ms(pk, torch, prod, launches=64, reps=5):
 
 # ------------------------------------------------------------ workloads ---
 
-def layer_step(pk, prods):
+def layer_step(pk, prods, packed=True):
     def fn():
         for p in prods:
-            p.quantize(pk)
-            p.gemm(pk)
+            if p.quantizes:
+                p.quantize(pk, packed=packed)
+            p.gemm(pk, packed=packed)
     return fn
 
 
@@ -194,6 +230,7 @@ def encoder_sweep(pk, torch, M, seed):
     ape = torch.from_numpy(synth.activations(g, 2 * M - 1, 1024)).to(dev)
     ape_q = torch.empty((2 * M - 1, 1024), dtype=torch.int8, device=dev)
     ape_d = torch.empty((2 * M - 1,), dtype=torch.float32, device=dev)
+    ape_qp = torch.empty((pk.packed_bytes(1024, 2 * M - 1),), dtype=torch.int8, device=dev)
     gain = lambda K: 1.0 / (np.sqrt(K) * 73.6 * 0.0055)   # noqa: E731
     order = ["ff1_up", "ff1_down", "q", "k", "v", "o", "pw1", "pw2", "ff2_up", "ff2_down"]
     shapes = {p[0]: p for p in synth.layer_products(M)}
@@ -209,14 +246,14 @@ def encoder_sweep(pk, torch, M, seed):
             prev, prev_xs = p.out, N
         _, mm, K, N, half, add = shapes["pos"]
         pp = Product(pk, torch, "pos", mm, K, N, half, add, g, x_dev=ape, xs=1024, ws_gain=gain(K))
-        pp.q, pp.d = ape_q, ape_d
+        pp.q, pp.d, pp.qp = ape_q, ape_d, ape_qp
         lay["pos"] = pp
         layers.append(lay)
         prev = lay["ff2_down"].out
         prev_xs = 1024
 
     def fn():
-        pk.quantize_dev(ape_q, ape_d, ape, 1024, 1024, 2 * M - 1, 1024)
+        pk.quantize_packed_dev(ape_q, ape_qp, ape_d, ape, 1024, 2 * M - 1, 1024)
         for lay in layers:
             for name in order[:5]:
                 lay[name].quantize(pk)
@@ -325,6 +362,24 @@ def cpu_baseline(prods_host, seconds):
     return results
 
 
+def recorded_traffic(kernel, M, K, N):
+    """HBM bytes a launch of this kernel on this shape, as the rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes summarized under profiles/ measured them
+    (each scaled by the same counter on a copy of known size); None when no
+    summary covers this kernel and shape."""
+    import glob
+    import re
+    want = f"kernel={kernel} M={M} K={K} N={N} "
+    for f in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.txt"))):
+        with open(f) as fh:
+            for line in fh:
+                if line.startswith("pmc: ") and want in line:
+                    m = re.search(r"traffic_bytes=(\d+)", line)
+                    if m:
+                        return int(m.group(1))
+    return None
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -345,21 +400,32 @@ def main():
               "(the int8 path would shard frames across GPUs with no exchange, DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     import torch
+    if args.copy_calibration:
+        a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copied_bytes": a.numel() * 4, "times": 3}))
+        return
     import libpktito_amd as pk
     pk.init()
     torch.cuda.set_device(0)
 
     M = 750
     prods = make_layer(pk, torch, M, seed=1)
-    step = layer_step(pk, prods)
-    graph = graph_of(torch, step)
     if args.profile_kernel:
+        # the named product's kernel alone, 50 times: what the rocprofv3
+        # summaries under profiles/ are cut from
         dom = next(p for p in prods if p.name == args.profile_kernel)
         for _ in range(50):
             dom.gemm(pk)
         torch.cuda.synchronize()
-        print(json.dumps({"profiled": dom.name, "kernel": pk.last_kernel()}))
+        print(json.dumps({"profiled": dom.name, "kernel": pk.last_kernel(), "launches": 50,
+                          "bytes_per_launch": dom.gemm_bytes()}))
         return
+    step = layer_step(pk, prods)
+    graph = graph_of(torch, step)
     log("layer M=750 captured")
     replay_ok = check_replay(pk, torch, prods, graph)
     ms = time_graph(torch, graph, args.steps, args.warmup)
@@ -382,7 +448,7 @@ def main():
                     achieved=round(achieved if bound == "hbm" else dom.ops() / (dkms * 1e-3) / 1e12, 1),
                     peak=HBM_PEAK_GBS if bound == "hbm" else MFMA_INT8_PEAK_TOPS,
                     kernel_us=round(dkms * 1e3, 3), bytes_per_launch=dbytes, ops_per_launch=dom.ops(),
-                    traffic=None)
+                    traffic=recorded_traffic(dname, dom.M, dom.K, dom.N))
     roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
     per_product = {p.name: dict(us=round(k * 1e3, 2), kernel=n,
                                 tops=round(p.ops() / (k * 1e-3) / 1e12, 1),
@@ -436,7 +502,7 @@ def main():
 
         def rag_step():
             for p, segs in rag:
-                p.quantize(pk)
+                p.quantize(pk, packed=False)
                 pk.gemm_q8_grouped_dev(p.m, 0, p.N, p.m.dev_scales, None, segs, p.add)
         grg = graph_of(torch, rag_step)
         rms = time_graph(torch, grg, 20, 3)
@@ -470,6 +536,82 @@ def main():
         extra["skinny"] = skinny_rates(pk, torch, [(1024, 4096, 4096), (4096, 1024, 1024), (640, 1040, 1030)])
 
         log("skinny done")
+
+        # the host-pointer drop-in (what backend/hip's table calls): host arrays
+        # in, host arrays out, every call staging activations and outputs over
+        # PCIe; the feed-forward up projection at M = 750
+        fu = next(p for p in prods if p.name == "ff1_up")
+        xh = fu.x_host.reshape(-1)
+        qh = np.zeros(fu.M * fu.K, np.int8)
+        dh = np.zeros(fu.M, np.float32)
+        oh = np.zeros(fu.M * fu.N, np.float32)
+        act = pk.make_act(qh, dh, fu.K, fu.K, fu.M)
+        pk.quantize(act, xh, fu.K)
+        pk.gemm_q8(oh, fu.N, fu.w, fu.ws, None, fu.N, act, 0)
+        reps = 20
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            pk.quantize(act, xh, fu.K)
+        tq = (time.perf_counter() - t0) / reps
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            pk.gemm_q8(oh, fu.N, fu.w, fu.ws, None, fu.N, act, 0)
+        tg = (time.perf_counter() - t0) / reps
+        # the same product dealt as the reference's pool deals it to 16
+        # threads (core/passes.c:28-46 and :80-109): quantize in 16-frame
+        # items, the product in slices of 64 or 256 rows, columns in chunks
+        # when that evens the last round; every call its own staging
+        nth = 16
+        pool = ThreadPoolExecutor(nth)
+        q_items = [(t0, min(16, fu.M - t0)) for t0 in range(0, fu.M, 16)]
+
+        def quant_item(it):
+            t0, nt = it
+            sub = pk.make_act(_addr(qh) + t0 * fu.K, _addr(dh) + 4 * t0, fu.K, fu.K, nt)
+            pk.quantize(sub, xh[t0 * fu.K:], fu.K)
+
+        step = 256 if fu.N // 256 >= 2 * nth else 64
+        rb = (fu.N + step - 1) // step
+        best, best_idle, best_all = 1, None, 1
+        for cc in range(1, 9):
+            if cc > 1 and fu.M // cc < 48:
+                break
+            items = rb * cc
+            alls = (items + nth - 1) // nth * nth
+            if best_idle is None or (alls - items) * best_all < best_idle * alls:
+                best, best_idle, best_all = cc, alls - items, alls
+        cstep = (fu.M + best - 1) // best
+        cstep = (cstep + 11) // 12 * 12 if best > 1 else fu.M
+        g_items = [(r0, min(step, fu.N - r0), c0, min(cstep, fu.M - c0))
+                   for c0 in range(0, fu.M, cstep) for r0 in range(0, fu.N, step)]
+
+        def gemm_item(it):
+            r0, nr, c0, nc = it
+            sub = pk.make_act(_addr(qh) + c0 * fu.K, _addr(dh) + 4 * c0, fu.K, fu.K, nc)
+            pk.gemm_q8(oh, fu.N, fu.w, fu.ws[r0:], None, nr, sub, 0, w_offset=r0 * fu.K,
+                       out_offset=c0 * fu.N + r0)
+
+        want = oh.copy()
+        list(pool.map(quant_item, q_items))
+        list(pool.map(gemm_item, g_items))
+        dealt_same = bool(np.array_equal(oh.view(np.uint32), want.view(np.uint32)))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            list(pool.map(quant_item, q_items))
+        tpq = (time.perf_counter() - t0) / reps
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            list(pool.map(gemm_item, g_items))
+        tpg = (time.perf_counter() - t0) / reps
+        pool.shutdown()
+        extra["host_drop_in_ff1_up_M750"] = dict(
+            one_call=dict(quantize_us=round(tq * 1e6, 1), gemm_q8_us=round(tg * 1e6, 1),
+                          tops=round(fu.ops() / tg / 1e12, 2)),
+            pool16=dict(quantize_us=round(tpq * 1e6, 1), quantize_calls=len(q_items),
+                        gemm_q8_us=round(tpg * 1e6, 1), gemm_q8_calls=len(g_items),
+                        tops=round(fu.ops() / tpg / 1e12, 2), same_bits_as_one_call=dealt_same),
+            note="host pointers: x or q, d H2D and out D2H over PCIe inside each call, through pinned staging")
+        log("host drop-in done")
         if not args.no_cpu:
             cpu = cpu_baseline(host_inputs, args.cpu_seconds)
             log("cpu baseline done")

@@ -76,7 +76,9 @@ int pk_hip_init(void);
  * panel inside it run on the device copy. rows % 16 == 0, cols % 32 == 0,
  * cols <= 16384 (core/model.c:354). Replaces nothing in the reference: it is
  * the step a GPU backend adds after core/model.c's load_file (:783-811). The
- * host bytes must not change while the matrix is uploaded. */
+ * host bytes and scales must not change while the matrix is uploaded (a
+ * model's are its mapped file's): gemm_q8 reads the device copies, the
+ * scales too when its ws is the uploaded s at that panel. */
 int pk_hip_upload_q8(const int8_t *q, const float *s, uint32_t rows, uint32_t cols);
 
 /* Frees the device copy of the matrix whose host bytes start at q
@@ -123,6 +125,29 @@ int pk_hip_quantize_dev(pk_hip_act *a, const float *x, size_t xs, void *stream);
 int pk_hip_gemm_q8_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
                        const float *ws, const float *bias, const pk_hip_act *a, int add,
                        int rmode, void *stream);
+
+/* Packed activations, for callers whose quantized activations feed only
+ * products: the frames in groups of 16 and each group's inputs in units of
+ * 16 frames x 64 inputs laid out as the MFMA takes them, unit u of every
+ * group before unit u + 1 (the repacked weights' layout), so that a
+ * product's activation tiles are contiguous 1 KB reads. Same q bytes, same
+ * d, same outputs as the row-major path. No counterpart in the reference,
+ * whose pk_act is row-major (backend/kernels.h:41-45): an extension of the
+ * device-resident path. */
+
+/* Bytes a packed copy of T columns of n inputs takes. */
+size_t pk_hip_packed_bytes(uint32_t n, uint32_t T);
+
+/* quantize (per-row blocks only: a->qb == a->n, n <= 4096) writing d and
+ * the packed copy qp, and the row-major a->q too unless it is NULL. Device
+ * pointers; qp 16-byte aligned and pk_hip_packed_bytes(n, T) long. */
+int pk_hip_quantize_packed_dev(pk_hip_act *a, int8_t *qp, const float *x, size_t xs, void *stream);
+
+/* gemm_q8_dev with the activations read from the packed copy qp (a->q is
+ * not read; a->d, n, qb == n and T are). */
+int pk_hip_gemm_q8_packed_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
+                              const float *ws, const float *bias, const pk_hip_act *a, const int8_t *qp,
+                              int add, int rmode, void *stream);
 
 /* One segment of a grouped product: its own activations and outputs. */
 typedef struct {

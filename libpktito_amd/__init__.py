@@ -74,6 +74,13 @@ _SIGS = {
     "pk_hip_gemm_q8_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_uint32,
                                           ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(Act),
                                           ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "pk_hip_packed_bytes": (ctypes.c_size_t, [ctypes.c_uint32, ctypes.c_uint32]),
+    "pk_hip_quantize_packed_dev": (ctypes.c_int, [ctypes.POINTER(Act), ctypes.c_void_p, ctypes.c_void_p,
+                                                  ctypes.c_size_t, ctypes.c_void_p]),
+    "pk_hip_gemm_q8_packed_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_uint32,
+                                                 ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
+                                                 ctypes.POINTER(Act), ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_void_p]),
     "pk_hip_gemm_q8_grouped_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                   ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(Seg),
                                                   ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]),
@@ -220,6 +227,26 @@ def gemm_q8_dev(out, os_, m, r0, rows, ws, bias, q, d, n, qb, T, add, rmode=0, s
     op = out_ptr if out_ptr is not None else _dptr(out)
     _check(lib().pk_hip_gemm_q8_dev(op, os_, m.handle, r0, rows, wsp, _dptr(bias),
                                     ctypes.byref(a), int(add), rmode, _stream(stream)))
+
+
+def packed_bytes(n, T):
+    """Bytes a packed copy of T columns of n inputs takes."""
+    return lib().pk_hip_packed_bytes(n, T)
+
+
+def quantize_packed_dev(q, qp, d, x, n, T, xs, stream=None):
+    """Per-row quantize on device tensors into the packed copy qp (uint8/int8,
+    packed_bytes(n, T) long), and into q [T, n] unless q is None."""
+    a = Act(_dptr(q), _dptr(d), n, n, T)
+    _check(lib().pk_hip_quantize_packed_dev(ctypes.byref(a), _dptr(qp), _dptr(x), xs, _stream(stream)))
+
+
+def gemm_q8_packed_dev(out, os_, m, r0, rows, ws_ptr, bias, qp, d, n, T, add, rmode=0, stream=None, out_ptr=None):
+    """gemm_q8 on device tensors with the activations from the packed copy qp."""
+    a = Act(None, _dptr(d), n, n, T)
+    op = out_ptr if out_ptr is not None else _dptr(out)
+    _check(lib().pk_hip_gemm_q8_packed_dev(op, os_, m.handle, r0, rows, ws_ptr, _dptr(bias), ctypes.byref(a),
+                                           _dptr(qp), int(add), rmode, _stream(stream)))
 
 
 def gemm_q8_grouped_dev(m, r0, rows, ws_ptr, bias, segs, add, stream=None):

@@ -13,6 +13,7 @@
 #include "pk_hip.h"
 #include "q8_internal.h"
 
+#include <algorithm>
 #include <cfenv>
 #include <cstdarg>
 #include <cstdio>
@@ -115,10 +116,21 @@ void free_matrix(pk_hip_q8 *m) {
 
 /* ----------------------------------------------------------- contexts --- */
 
+/* Host memory that a DMA copy reads or writes must be pinned, and the
+ * caller's buffers are not (a mapped model file, malloc'd activations); a
+ * copy from pageable memory, and worse a pitched one, runs far below the
+ * link's rate. So each context holds two pinned slots: rows are gathered
+ * into one on the CPU while the other's DMA runs, and outputs come back the
+ * same way in reverse. */
+constexpr size_t kSlot = (size_t)4 << 20;
+
 struct Ctx {
     hipStream_t stream = nullptr;
     char *dev = nullptr;
     size_t cap = 0;
+    char *host[2] = { nullptr, nullptr };
+    hipEvent_t ev[2] = { nullptr, nullptr };
+    bool used[2] = { false, false };        /* ev[i] was recorded */
 };
 
 std::mutex g_ctx_mu;
@@ -146,11 +158,104 @@ int lease(Lease &l) {
     if (!l.c) {
         Ctx *c = new Ctx;
         hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+        for (int i = 0; i < 2 && e == hipSuccess; i++) {
+            e = hipHostMalloc((void **)&c->host[i], kSlot, hipHostMallocDefault);
+            if (e == hipSuccess)
+                e = hipEventCreateWithFlags(&c->ev[i], hipEventDisableTiming);
+        }
         if (e != hipSuccess) {
+            for (int i = 0; i < 2; i++) {
+                if (c->ev[i]) (void)hipEventDestroy(c->ev[i]);
+                if (c->host[i]) (void)hipHostFree(c->host[i]);
+            }
+            if (c->stream) (void)hipStreamDestroy(c->stream);
             delete c;
-            return hip_fail(e, "hipStreamCreateWithFlags");
+            return hip_fail(e, "making a staging context");
         }
         l.c = c;
+    }
+    return PK_HIP_OK;
+}
+
+/* Bytes [b0, b0 + len) of a T x rowbytes block held with a pitch, to or from
+ * dense memory: row by row, one memcpy when the pitch is the row. */
+void gather(char *dense, const char *src, size_t b0, size_t len, size_t rowbytes, size_t pitch) {
+    if (pitch == rowbytes) {
+        memcpy(dense, src + b0, len);
+        return;
+    }
+    while (len) {
+        const size_t r = b0 / rowbytes, o = b0 % rowbytes, k = std::min(len, rowbytes - o);
+        memcpy(dense, src + r * pitch + o, k);
+        dense += k;
+        b0 += k;
+        len -= k;
+    }
+}
+
+void scatter(char *dst, const char *dense, size_t b0, size_t len, size_t rowbytes, size_t pitch) {
+    if (pitch == rowbytes) {
+        memcpy(dst + b0, dense, len);
+        return;
+    }
+    while (len) {
+        const size_t r = b0 / rowbytes, o = b0 % rowbytes, k = std::min(len, rowbytes - o);
+        memcpy(dst + r * pitch + o, dense, k);
+        dense += k;
+        b0 += k;
+        len -= k;
+    }
+}
+
+int slot_free(Ctx *c, int i) {
+    if (c->used[i])
+        PK_TRY(hipEventSynchronize(c->ev[i]));
+    return PK_HIP_OK;
+}
+
+/* nrows rows of rowbytes from host src (a row every pitch bytes; pitch is
+ * not read for one row) to dense device memory at dst, on c's stream. */
+int h2d(Ctx *c, void *dst, const void *src, size_t rowbytes, size_t nrows, size_t pitch) {
+    const size_t total = rowbytes * nrows;
+    int e;
+    for (size_t b0 = 0, k = 0; b0 < total; b0 += kSlot, k++) {
+        const int i = (int)(k & 1);
+        const size_t len = std::min(kSlot, total - b0);
+        if ((e = slot_free(c, i)))
+            return e;
+        gather(c->host[i], (const char *)src, b0, len, rowbytes, pitch);
+        PK_TRY(hipMemcpyAsync((char *)dst + b0, c->host[i], len, hipMemcpyHostToDevice, c->stream));
+        PK_TRY(hipEventRecord(c->ev[i], c->stream));
+        c->used[i] = true;
+    }
+    return PK_HIP_OK;
+}
+
+/* The reverse: dense device src, after the stream's earlier work, to host
+ * dst with a pitch; returns with the bytes in place. */
+int d2h(Ctx *c, void *dst, size_t pitch, const void *src, size_t rowbytes, size_t nrows) {
+    const size_t total = rowbytes * nrows, n = (total + kSlot - 1) / kSlot;
+    int e;
+    auto issue = [&](size_t k) -> int {
+        const int i = (int)(k & 1);
+        const size_t b0 = k * kSlot, len = std::min(kSlot, total - b0);
+        if ((e = slot_free(c, i)))
+            return e;
+        PK_TRY(hipMemcpyAsync(c->host[i], (const char *)src + b0, len, hipMemcpyDeviceToHost, c->stream));
+        PK_TRY(hipEventRecord(c->ev[i], c->stream));
+        c->used[i] = true;
+        return PK_HIP_OK;
+    };
+    for (size_t k = 0; k < n && k < 2; k++)
+        if ((e = issue(k)))
+            return e;
+    for (size_t k = 0; k < n; k++) {
+        const int i = (int)(k & 1);
+        const size_t b0 = k * kSlot, len = std::min(kSlot, total - b0);
+        PK_TRY(hipEventSynchronize(c->ev[i]));
+        scatter((char *)dst, c->host[i], b0, len, rowbytes, pitch);
+        if (k + 2 < n && (e = issue(k + 2)))
+            return e;
     }
     return PK_HIP_OK;
 }
@@ -218,7 +323,7 @@ int launch_quant(pk_hip_act *a, const float *x, size_t xs, hipStream_t s) {
 
 int launch_product(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
                    const float *ws, const float *bias, const pk_hip_act *a, int add, int rmode,
-                   hipStream_t s) {
+                   hipStream_t s, const int8_t *qp = nullptr) {
     pkq8::GemmArgs g;
     g.w = m->w + (size_t)(r0 / 16) * pkq8::kUnitBytes;
     g.wstride = (uint64_t)(m->rows / 16) * pkq8::kUnitBytes;
@@ -234,7 +339,8 @@ int launch_product(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint3
     g.rmode = rmode;
     pkq8::SegTable tab;
     tab.nseg = 1;
-    tab.s[0] = pkq8::Seg{ out, a->q, a->d, (uint64_t)os, a->T, 0 };
+    tab.s[0] = pkq8::Seg{ out, qp ? qp : a->q, a->d, (uint64_t)os,
+                          qp ? (uint64_t)pkq8::packed_groups(a->T) * pkq8::kUnitBytes : 0, a->T, 0 };
     const char *name = "";
     if (pkq8::launch_gemm(g, tab, s, &name))
         return hip_fail(hipGetLastError(), "gemm_q8 launch");
@@ -382,14 +488,13 @@ int pk_hip_quantize(pk_hip_act *a, const float *x, size_t xs) {
     int8_t *dq = (int8_t *)(l.c->dev + xb);
     float *dd = (float *)(l.c->dev + xb + qbytes);
     hipStream_t s = l.c->stream;
-    PK_TRY(hipMemcpy2DAsync(dx, n * sizeof(float), x, xs * sizeof(float), n * sizeof(float), T,
-                            hipMemcpyHostToDevice, s));
+    if ((e = h2d(l.c, dx, x, n * sizeof(float), T, xs * sizeof(float))))
+        return e;
     pk_hip_act da = { dq, dd, a->n, a->qb, a->T };
     if ((e = launch_quant(&da, dx, n, s)))
         return e;
-    PK_TRY(hipMemcpyAsync(a->q, dq, T * n, hipMemcpyDeviceToHost, s));
-    PK_TRY(hipMemcpyAsync(a->d, dd, T * nb * sizeof(float), hipMemcpyDeviceToHost, s));
-    PK_TRY(hipStreamSynchronize(s));
+    if ((e = d2h(l.c, a->q, n, dq, n, T)) || (e = d2h(l.c, a->d, nb * sizeof(float), dd, nb * sizeof(float), T)))
+        return e;
     return PK_HIP_OK;
 }
 
@@ -437,26 +542,24 @@ int pk_hip_gemm_q8(float *out, size_t os, const int8_t *w, const float *ws, cons
     float *db = (float *)(p + bq + bd + bw);
     float *dout = (float *)(p + bq + bd + 2 * bw);
     hipStream_t s = l.c->stream;
-    PK_TRY(hipMemcpyAsync(dq, a->q, T * n, hipMemcpyHostToDevice, s));
-    PK_TRY(hipMemcpyAsync(dd, a->d, T * nb * 4, hipMemcpyHostToDevice, s));
-    PK_TRY(hipMemcpyAsync(dws, ws, R * 4, hipMemcpyHostToDevice, s));
-    if (bias)
-        PK_TRY(hipMemcpyAsync(db, bias, R * 4, hipMemcpyHostToDevice, s));
-    if (add) {
-        if (T == 1)
-            PK_TRY(hipMemcpyAsync(dout, out, R * 4, hipMemcpyHostToDevice, s));
-        else
-            PK_TRY(hipMemcpy2DAsync(dout, R * 4, out, os * 4, R * 4, T, hipMemcpyHostToDevice, s));
-    }
-    pk_hip_act da = { dq, dd, a->n, a->qb, a->T };
-    if ((e = launch_product(dout, R, m, r0, rows, dws, bias ? db : nullptr, &da, add, rmode, s)))
+    if ((e = h2d(l.c, dq, a->q, T * n, 1, 0)) || (e = h2d(l.c, dd, a->d, T * nb * 4, 1, 0)))
         return e;
-    if (T == 1)
-        PK_TRY(hipMemcpyAsync(out, dout, R * 4, hipMemcpyDeviceToHost, s));
-    else
-        PK_TRY(hipMemcpy2DAsync(out, os * 4, dout, R * 4, R * 4, T, hipMemcpyDeviceToHost, s));
-    PK_TRY(hipStreamSynchronize(s));
-    return PK_HIP_OK;
+    /* the scales a model binds are the uploaded matrix's own, already on the
+     * device; other scales are copied */
+    const float *wsd = m->s + r0;
+    if (ws != m->hs + r0) {
+        if ((e = h2d(l.c, dws, ws, R * 4, 1, 0)))
+            return e;
+        wsd = dws;
+    }
+    if (bias && (e = h2d(l.c, db, bias, R * 4, 1, 0)))
+        return e;
+    if (add && (e = h2d(l.c, dout, out, R * 4, T, os * 4)))
+        return e;
+    pk_hip_act da = { dq, dd, a->n, a->qb, a->T };
+    if ((e = launch_product(dout, R, m, r0, rows, wsd, bias ? db : nullptr, &da, add, rmode, s)))
+        return e;
+    return d2h(l.c, out, os * 4, dout, R * 4, T);
 }
 
 int pk_hip_quantize_dev(pk_hip_act *a, const float *x, size_t xs, void *stream) {
@@ -497,6 +600,53 @@ int pk_hip_gemm_q8_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, u
     return launch_product(out, os, m, r0, rows, ws, bias, a, add, rmode, (hipStream_t)stream);
 }
 
+size_t pk_hip_packed_bytes(uint32_t n, uint32_t T) { return (size_t)pkq8::packed_bytes(n, T); }
+
+int pk_hip_quantize_packed_dev(pk_hip_act *a, int8_t *qp, const float *x, size_t xs, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!a)
+        return fail(PK_HIP_EINVAL, "quantize_packed_dev: act is NULL");
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!a->d || !qp || a->qb != a->n || a->n == 0 || a->n % 32 || a->n > 4096)
+        return fail(PK_HIP_EINVAL, "quantize_packed_dev: per-row blocks (qb == n), n a multiple of 32 "
+                                   "up to 4096, d and qp set");
+    if (xs < a->n || xs % 4 || ((uintptr_t)x & 15) || ((uintptr_t)qp & 15) || ((uintptr_t)a->q & 15))
+        return fail(PK_HIP_EINVAL, "quantize_packed_dev: x, q and qp 16-byte aligned, xs >= n and a multiple of 4");
+    const char *name = "";
+    if (pkq8::launch_quantize_packed(a->q, qp, a->d, x, xs, a->n, a->T, (hipStream_t)stream, &name))
+        return hip_fail(hipGetLastError(), "quantize_packed launch");
+    g_kernel = name;
+    return PK_HIP_OK;
+}
+
+int pk_hip_gemm_q8_packed_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
+                              const float *ws, const float *bias, const pk_hip_act *a, const int8_t *qp,
+                              int add, int rmode, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!m)
+        return fail(PK_HIP_ENOTUP, "gemm_q8_packed_dev: no matrix");
+    if (!a)
+        return fail(PK_HIP_EINVAL, "gemm_q8_packed_dev: act is NULL");
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!a->d || !qp || ((uintptr_t)qp & 15) || a->qb != a->n || a->n % 32 || a->n > 16384)
+        return fail(PK_HIP_EINVAL, "gemm_q8_packed_dev: per-row blocks (qb == n), d and a 16-byte aligned qp");
+    if (!out || !ws)
+        return fail(PK_HIP_EINVAL, "gemm_q8_packed_dev: out or ws is NULL");
+    if (a->T > 1 && os < rows)
+        return fail(PK_HIP_EINVAL, "gemm_q8_packed_dev: output stride %zu is under rows %u", os, rows);
+    if (rmode < 0 || rmode > 3)
+        return fail(PK_HIP_EROUND, "gemm_q8_packed_dev: rmode %d", rmode);
+    if ((e = check_panel(m, r0, rows, a->n)))
+        return e;
+    return launch_product(out, os, m, r0, rows, ws, bias, a, add, rmode, (hipStream_t)stream, qp);
+}
+
 int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, const float *ws,
                                const float *bias, const pk_hip_seg *segs, uint32_t nseg, int add,
                                void *stream) {
@@ -523,7 +673,7 @@ int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, c
                         sg.a.n, sg.a.qb, n, qb);
         if (!sg.out || ((uintptr_t)sg.a.q & 15) || (sg.a.T > 1 && sg.os < rows))
             return fail(PK_HIP_EINVAL, "gemm_q8_grouped_dev: segment %u: out NULL, q unaligned or os < rows", i);
-        tab.s[tab.nseg++] = pkq8::Seg{ sg.out, sg.a.q, sg.a.d, (uint64_t)sg.os, sg.a.T, 0 };
+        tab.s[tab.nseg++] = pkq8::Seg{ sg.out, sg.a.q, sg.a.d, (uint64_t)sg.os, 0, sg.a.T, 0 };
     }
     if (tab.nseg == 0)
         return PK_HIP_OK;

@@ -29,12 +29,24 @@ inline uint32_t units_per_panel(uint32_t cols) { return (units_with_data(cols) +
 /* One segment of activations and outputs. */
 struct Seg {
     float *out;
-    const int8_t *q;
+    const int8_t *q;            /* row-major [T][n], or packed units when qstride != 0 */
     const float *d;
     uint64_t os;
+    uint64_t qstride;           /* packed: bytes from a row group's unit u to its unit u + 1 */
     uint32_t T;
     uint32_t tile0;             /* the grouped launch's first M tile of this segment */
 };
+
+/* Packed activations: the frames in groups of 16, each group's inputs in
+ * units of 64 like the weights (16 rows x 64 inputs, 1 KB, MFMA operand
+ * order), stage-major: unit (g, u) at 1 KB * (u * G + g), G = ceil(T / 16),
+ * ku units a group as for a matrix of n inputs. Rows past T and inputs past
+ * n are left unwritten: rows past T are never stored, and inputs past n meet
+ * zero weights. */
+inline uint32_t packed_groups(uint32_t T) { return (T + 15) / 16; }
+inline uint64_t packed_bytes(uint32_t n, uint32_t T) {
+    return (uint64_t)packed_groups(T) * units_per_panel(n) * kUnitBytes;
+}
 
 constexpr int kMaxSegs = 64;
 
@@ -61,6 +73,11 @@ int launch_repack(int8_t *dst, const int8_t *src, uint32_t rows, uint32_t cols, 
 
 int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb,
                     uint32_t T, hipStream_t s, const char **name);
+
+/* Per-row quantize (qb == n, n <= 4096) writing the packed copy qp, and the
+ * row-major q too when q is not NULL. */
+int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
+                           uint32_t T, hipStream_t s, const char **name);
 
 /* The pipelined product's tilings: how many, and forcing one (-1: the
  * heuristic); returns the one forced before. */

@@ -190,10 +190,10 @@ __global__ __launch_bounds__(256) void quant_any_kernel(int8_t *__restrict__ q, 
 /* A whole column is one block, n <= 4096: one wave a column, four columns a
  * workgroup, each lane CH float4 chunks of it (chunk c of lane l is float4
  * l + 64 c), every load issued before the first is used. */
-template <int CH>
-__global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q, float *__restrict__ d,
-                                                         const float *__restrict__ x, size_t xs,
-                                                         uint32_t n, uint32_t T) {
+template <int CH, bool PACK>
+__global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q, int8_t *__restrict__ qp,
+                                                         float *__restrict__ d, const float *__restrict__ x,
+                                                         size_t xs, uint32_t n, uint32_t T) {
     const int lane = threadIdx.x & 63;
     const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T)
@@ -223,14 +223,41 @@ __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q,
         id = 127.0f / amax;
     }
     int *qr = (int *)(q + (size_t)t * n);
+    /* packed: row t is row t % 16 of group t / 16; inputs k..k+3 of unit
+     * k / 64 sit at 16 (16 kq + r) + k % 16, kq = (k % 64) / 16 */
+    const uint32_t G = (T + 15) / 16, g = t >> 4, r = t & 15;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
-        if (i < n4)
-            qr[i] = zero ? 0 : pack4(v[c], id);
+        if (i < n4) {
+            const int v4 = zero ? 0 : pack4(v[c], id);
+            if (!PACK || q)
+                qr[i] = v4;
+            if (PACK) {
+                const uint32_t k = 4 * i, u = k >> 6, kq = (k >> 4) & 3;
+                *(int *)(qp + ((size_t)u * G + g) * kUnitBytes + (kq * 16 + r) * 16 + (k & 15)) = v4;
+            }
+        }
     }
     if (lane == 0)
         d[t] = dv;
+}
+
+int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
+                           uint32_t T, hipStream_t s, const char **name) {
+    if (T == 0)
+        return 0;
+    const uint32_t n4 = n / 4, grid4 = (T + 3) / 4;
+    if (n4 <= 256) {
+        quant_wave_kernel<4, true><<<grid4, 256, 0, s>>>(q, qp, d, x, xs, n, T);
+        *name = "quant_wave_packed<4>";
+    } else if (n4 <= 1024) {
+        quant_wave_kernel<16, true><<<grid4, 256, 0, s>>>(q, qp, d, x, xs, n, T);
+        *name = "quant_wave_packed<16>";
+    } else {
+        return -2;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb,
@@ -239,10 +266,10 @@ int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, 
         return 0;
     const uint32_t nch = n / 16, n4 = n / 4, grid4 = (T + 3) / 4;
     if (qb == n && n4 <= 256) {
-        quant_wave_kernel<4><<<grid4, 256, 0, s>>>(q, d, x, xs, n, T);
+        quant_wave_kernel<4, false><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
         *name = "quant_wave<4>";
     } else if (qb == n && n4 <= 1024) {
-        quant_wave_kernel<16><<<grid4, 256, 0, s>>>(q, d, x, xs, n, T);
+        quant_wave_kernel<16, false><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
         *name = "quant_wave<16>";
     } else if (qb == n && nch <= 1024) {
         quant_col_kernel<4, 4><<<T, 256, 0, s>>>(q, d, x, xs, n);
@@ -556,7 +583,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_q8_grouped_kernel(GemmArgs 
  * units between them, each reading its weight units straight from HBM (1 KB
  * contiguous a wave a unit) and the frames' inputs from L2, and their int32
  * sums meet in LDS. Per-row blocks only (MODE 0). */
-template <int KW>
+template <int KW, bool PACKED>
 __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg sg) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t p = blockIdx.x, n = g.n, ku = g.ku, kr = g.kr, T = sg.T;
@@ -566,22 +593,23 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
     const size_t ws_ = g.wstride;
     uint32_t row = lane & 15;
     row = row < T ? row : T - 1;
-    const int8_t *ap = sg.q + (size_t)row * n;
+    /* packed: the frames are one group, unit u at qstride u, lane-ordered */
+    const int8_t *ap = PACKED ? sg.q + lane * 16 : sg.q + (size_t)row * n;
     v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
     uint32_t u = wave;
     for (; u + KW < kr; u += 2 * KW) {
         const v4i w0 = *(const v4i *)(wp + (size_t)u * ws_);
         const v4i w1 = *(const v4i *)(wp + (size_t)(u + KW) * ws_);
         const uint32_t k0 = u * 64 + (lane >> 4) * 16, k1 = k0 + KW * 64;
-        const v4i a0 = *(const v4i *)(ap + (k0 < n ? k0 : 0));
-        const v4i a1 = *(const v4i *)(ap + (k1 < n ? k1 : 0));
+        const v4i a0 = *(const v4i *)(ap + (PACKED ? (size_t)u * sg.qstride : (k0 < n ? k0 : 0)));
+        const v4i a1 = *(const v4i *)(ap + (PACKED ? (size_t)(u + KW) * sg.qstride : (k1 < n ? k1 : 0)));
         acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0, a0, acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w1, a1, acc1, 0, 0, 0);
     }
     if (u < kr) {
         const v4i w0 = *(const v4i *)(wp + (size_t)u * ws_);
         const uint32_t k0 = u * 64 + (lane >> 4) * 16;
-        const v4i a0 = *(const v4i *)(ap + (k0 < n ? k0 : 0));
+        const v4i a0 = *(const v4i *)(ap + (PACKED ? (size_t)u * sg.qstride : (k0 < n ? k0 : 0)));
         acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0, a0, acc0, 0, 0, 0);
     }
     __shared__ v4i red[KW][64];
@@ -663,7 +691,7 @@ __device__ __forceinline__ void wait_lgkm() {
  * panels and UA frame groups: slot layout [kk < UPS][unit < UA + UB], 1 KB a
  * unit. Within a stage the fragments of sub-step kk + 1 are read while the
  * MFMAs of sub-step kk run (two register sets). */
-template <int WN, int WM, int TN, int TM, int UPS>
+template <int WN, int WM, int TN, int TM, int UPS, bool PACKED>
 __device__ __forceinline__ void ring_tile(const GemmArgs &g, const Seg &sg, uint32_t tn, uint32_t tm) {
     constexpr int NW = WN * WM;
     constexpr int BN = 16 * TN * WN, BM = 16 * TM * WM;
@@ -702,6 +730,12 @@ __device__ __forceinline__ void ring_tile(const GemmArgs &g, const Seg &sg, uint
             p = p < npan ? p : npan - 1;
             src[s] = g.w + (size_t)p * kUnitBytes + lane * 16;
             isw[s] = true;
+        } else if (PACKED) {
+            const uint32_t ng = (T + 15) / 16;
+            uint32_t gi = m0 / 16 + (u - UB);
+            gi = gi < ng ? gi : ng - 1;
+            src[s] = sg.q + (size_t)gi * kUnitBytes + lane * 16;
+            isw[s] = false;
         } else {
             uint32_t row = m0 + (u - UB) * 16 + (lane & 15);
             row = row < T ? row : T - 1;
@@ -716,6 +750,8 @@ __device__ __forceinline__ void ring_tile(const GemmArgs &g, const Seg &sg, uint
             const int8_t *gp;
             if (isw[s]) {
                 gp = src[s] + (size_t)unit * g.wstride;
+            } else if (PACKED) {
+                gp = src[s] + (size_t)unit * sg.qstride;
             } else {
                 /* inputs past n: the row's first 16, against zero weights */
                 const uint32_t k = unit * 64 + (lane >> 4) * 16;
@@ -864,31 +900,31 @@ __device__ __forceinline__ void xcd_tile(uint32_t b, uint32_t nwg, uint32_t tile
     tn = idx / gm;
 }
 
-template <int WN, int WM, int TN, int TM, int UPS>
+template <int WN, int WM, int TN, int TM, int UPS, bool PACKED>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_ring_kernel(GemmArgs g, Seg sg, uint32_t tiles_n,
                                                                  uint32_t tiles_m) {
     uint32_t tn, tm;
     xcd_tile(blockIdx.x, gridDim.x, tiles_n, tiles_m, tn, tm);
-    ring_tile<WN, WM, TN, TM, UPS>(g, sg, tn, tm);
+    ring_tile<WN, WM, TN, TM, UPS, PACKED>(g, sg, tn, tm);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS>
+template <int WN, int WM, int TN, int TM, int UPS, bool PACKED>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_ring_grouped_kernel(GemmArgs g, SegTable tab,
                                                                          uint32_t tiles_n) {
     const uint32_t tm = blockIdx.x / tiles_n;
     uint32_t i = 0;
     while (i + 1 < tab.nseg && tab.s[i + 1].tile0 <= tm)
         i++;
-    ring_tile<WN, WM, TN, TM, UPS>(g, tab.s[i], blockIdx.x % tiles_n, tm - tab.s[i].tile0);
+    ring_tile<WN, WM, TN, TM, UPS, PACKED>(g, tab.s[i], blockIdx.x % tiles_n, tm - tab.s[i].tile0);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS>
-static void run_ring(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
+template <int WN, int WM, int TN, int TM, int UPS, bool PACKED>
+static void run_ring1(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
     constexpr uint32_t BN = 16 * TN * WN, BM = 16 * TM * WM;
     const uint32_t tiles_n = (g.rows + BN - 1) / BN;
     if (tab.nseg == 1) {
         const uint32_t tiles_m = (tab.s[0].T + BM - 1) / BM;
-        gemm_ring_kernel<WN, WM, TN, TM, UPS><<<tiles_n * tiles_m, 64 * WN * WM, 0, s>>>(g, tab.s[0], tiles_n, tiles_m);
+        gemm_ring_kernel<WN, WM, TN, TM, UPS, PACKED><<<tiles_n * tiles_m, 64 * WN * WM, 0, s>>>(g, tab.s[0], tiles_n, tiles_m);
     } else {
         SegTable t = tab;
         uint32_t tiles = 0;
@@ -896,8 +932,16 @@ static void run_ring(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
             t.s[i].tile0 = tiles;
             tiles += (t.s[i].T + BM - 1) / BM;
         }
-        gemm_ring_grouped_kernel<WN, WM, TN, TM, UPS><<<tiles_n * tiles, 64 * WN * WM, 0, s>>>(g, t, tiles_n);
+        gemm_ring_grouped_kernel<WN, WM, TN, TM, UPS, PACKED><<<tiles_n * tiles, 64 * WN * WM, 0, s>>>(g, t, tiles_n);
     }
+}
+
+template <int WN, int WM, int TN, int TM, int UPS>
+static void run_ring(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
+    if (tab.s[0].qstride)
+        run_ring1<WN, WM, TN, TM, UPS, true>(g, tab, s);
+    else
+        run_ring1<WN, WM, TN, TM, UPS, false>(g, tab, s);
 }
 
 /* The pipelined product's tile shapes: channels x frames, and the units of
@@ -921,6 +965,7 @@ static const RingCfg kRing[] = {
     { "ring<256x256w8,1>", 256, 256, 1, run_ring<2, 4, 8, 4, 1> },
     { "ring<256x128w4,1>", 256, 128, 1, run_ring<2, 2, 8, 4, 1> },
     { "ring<128x256w4,1>", 128, 256, 1, run_ring<2, 2, 4, 8, 1> },
+    { "ring<128x256w8,1>", 128, 256, 1, run_ring<2, 4, 4, 4, 1> },
 };
 constexpr int kNRing = sizeof kRing / sizeof kRing[0];
 
@@ -941,10 +986,17 @@ static int pick_ring(uint32_t rows, uint64_t frames, uint32_t ku) {
     if (g_forced_ring >= 0 && ku % (4 * kRing[g_forced_ring].ups) == 0)
         return g_forced_ring;
     auto tiles = [&](int i) { return (uint64_t)((rows + kRing[i].bn - 1) / kRing[i].bn) * ((frames + kRing[i].bm - 1) / kRing[i].bm); };
-    if (tiles(0) >= 512)
+    /* measured on the layer's shapes at 750 and 7500 frames: deep inputs
+     * (K >= 2048) with a CU's worth of 128 x 128 tiles take those; otherwise
+     * 64 x 64 tiles, with longer stages the fewer the tiles (more of a
+     * workgroup's loads in flight where workgroups are few) */
+    if (ku >= 32 && tiles(0) >= 256)
         return 0;
-    if (tiles(5) >= 256 && ku % 8 == 0)
-        return 5;
+    const uint64_t t64 = tiles(2);
+    if (t64 >= 512)
+        return 2;
+    if (t64 >= 256 && ku % 8 == 0)
+        return 3;
     return ku % 16 == 0 ? 4 : ku % 8 == 0 ? 3 : 2;
 }
 
@@ -990,12 +1042,19 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
     static thread_local char buf[96];
     if (mode == 0 && tab.nseg == 1 && tmax <= 16) {
         const uint32_t panels = g.rows / 16;
+        const bool packed = tab.s[0].qstride != 0;
         if (g.ku >= 32) {
-            gemm_q8_skinny_kernel<8><<<panels, 512, 0, s>>>(g, tab.s[0]);
-            *name = "skinny<8>";
+            if (packed)
+                gemm_q8_skinny_kernel<8, true><<<panels, 512, 0, s>>>(g, tab.s[0]);
+            else
+                gemm_q8_skinny_kernel<8, false><<<panels, 512, 0, s>>>(g, tab.s[0]);
+            *name = packed ? "skinny_packed<8>" : "skinny<8>";
         } else {
-            gemm_q8_skinny_kernel<4><<<panels, 256, 0, s>>>(g, tab.s[0]);
-            *name = "skinny<4>";
+            if (packed)
+                gemm_q8_skinny_kernel<4, true><<<panels, 256, 0, s>>>(g, tab.s[0]);
+            else
+                gemm_q8_skinny_kernel<4, false><<<panels, 256, 0, s>>>(g, tab.s[0]);
+            *name = packed ? "skinny_packed<4>" : "skinny<4>";
         }
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }

@@ -89,3 +89,28 @@ def test_missing_library_raises(tmp_path, monkeypatch):
     monkeypatch.setattr(pk, "_lib", None)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         pk.lib()
+
+
+REF = "/root/reference"
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(REF, "backend", "kernels.h")),
+                    reason="the reference checkout is not here")
+@pytest.mark.parametrize("src", ["kernels.c", "model_upload.c"])
+def test_drop_in_compiles_against_the_reference(src, tmp_path):
+    """The backend table and the model-load step, compiled as C11 with the
+    reference's own flags against its headers (backend/kernels.h, core/model.h),
+    as they would be in backend/hip/ and core/."""
+    path = os.path.join(ROOT, "libpktito_amd", "backend_hip", src)
+    cmd = ["gcc", "-std=c11", "-O2", "-ffp-contract=off", "-fno-math-errno", "-Wall", "-Wextra", "-Werror",
+           "-Wpedantic", "-D_DEFAULT_SOURCE", "-D_POSIX_C_SOURCE=200809L",
+           "-I", os.path.join(REF, "backend"), "-I", os.path.join(REF, "core"), "-I", os.path.join(ROOT, "include"),
+           "-c", path, "-o", str(tmp_path / (src + ".o"))]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    syms = subprocess.run(["nm", str(tmp_path / (src + ".o"))], capture_output=True, text=True).stdout
+    if src == "kernels.c":
+        assert " R pk_kernels_hip" in syms or " D pk_kernels_hip" in syms
+        assert "U pk_hip_gemm_q8" in syms and "U pk_hip_quantize" in syms
+    else:
+        assert " T pk_hip_upload_model" in syms and " T pk_hip_release_model" in syms

@@ -154,3 +154,54 @@ def test_interior_panels_device(hip, torch):
     want_nob = old.copy()
     ol.gemm_q8(want_nob, os_, w, ws, None, rows, q, d, K, K, M, 1, r0=r0)
     assert np.array_equal(bits(ot.cpu().numpy()), bits(want_nob))
+
+
+def unpack_packed(qp, n, T):
+    """Packed activations (16-frame groups, units of 16 x 64 in MFMA order,
+    stage-major) back to row-major [T, n]."""
+    G = (T + 15) // 16
+    ku = len(qp) // (G * 1024)
+    u = qp.reshape(ku, G, 4, 16, 16)            # [unit][group][kq][row][16 bytes]
+    full = u.transpose(1, 3, 0, 2, 4).reshape(G * 16, ku * 64)
+    return full[:T, :n]
+
+
+@pytest.mark.parametrize("M,K,N", [(750, 1024, 4096), (1499, 1024, 1024), (300, 4096, 1024), (16, 1024, 4096),
+                                   (5, 640, 1040), (97, 640, 208)])
+def test_packed_path(hip, torch, M, K, N):
+    """The packed-activation path: its q and d are the oracle's, its packed
+    copy holds the same bytes, and every tiling's products are the bits of
+    the row-major path and of the oracle."""
+    g = synth.rng(M * 3 + K)
+    w = synth.pack_q8(synth.weights(g, N, K))
+    ws = synth.scales(g, N)
+    x = synth.activations(g, M, K)
+    dev = torch.device("cuda")
+    xt = torch.from_numpy(x).to(dev)
+    qt = torch.empty((M, K), dtype=torch.int8, device=dev)
+    dt = torch.empty((M,), dtype=torch.float32, device=dev)
+    qp = torch.zeros((hip.packed_bytes(K, M),), dtype=torch.int8, device=dev)
+    say("packed quantize", M, K, N)
+    hip.quantize_packed_dev(qt, qp, dt, xt, K, M, K)
+    torch.cuda.synchronize()
+    q, d = ol.quantize(x.reshape(-1), M, K, K, K)
+    assert np.array_equal(qt.cpu().numpy().reshape(-1), q) and np.array_equal(bits(dt.cpu().numpy()), bits(d))
+    assert np.array_equal(unpack_packed(qp.cpu().numpy(), K, M), q.reshape(M, K))
+    frames = np.unique(np.concatenate([[0, M - 1], synth.rng(M).integers(0, M, 32)]))
+    want = sampled_oracle(q, d, w, ws, None, K, N, frames)
+    with hip.Q8Matrix(w, ws) as m:
+        ref = torch.empty((M, N), dtype=torch.float32, device=dev)
+        hip.gemm_q8_dev(ref, N, m, 0, N, None, None, qt, dt, K, K, M, 0, ws_ptr=m.dev_scales)
+        torch.cuda.synchronize()
+        r = ref.cpu().numpy()
+        assert np.array_equal(bits(r[frames]), bits(want))
+        try:
+            for ti in [-1] + list(range(hip.tilings())):
+                hip.force_tiling(ti)
+                out = torch.full((M, N), 3.0, dtype=torch.float32, device=dev)
+                say("packed product", ti, M, K, N)
+                hip.gemm_q8_packed_dev(out, N, m, 0, N, m.dev_scales, None, qp, dt, K, M, 0)
+                torch.cuda.synchronize()
+                assert np.array_equal(bits(out.cpu().numpy()), bits(r)), (ti, hip.last_kernel())
+        finally:
+            hip.force_tiling(-1)

@@ -253,6 +253,33 @@ def test_split_invariance_and_threads(hip):
     assert same(out, whole)
 
 
+def test_host_staging(hip):
+    """The host-pointer pair moves data through two pinned 4 MiB slots: inputs
+    and outputs of several slots' worth, with pitches (xs > n, os > rows),
+    add's read of out, and scales other than the uploaded ones (copied per
+    call) all give the oracle's bits."""
+    g = synth.rng(77)
+    M, K, N = 2400, 960, 1040         # x 9.2 MB, out 10 MB: three slots each, rows split across slots
+    xs, os_ = K + 8, N + 5
+    x = g.standard_normal(M * xs).astype(np.float32)
+    say("staging quantize", M, K, xs)
+    q, d = hip_quantize(hip, x, M, K, K, xs)
+    q2, d2 = ol.quantize(x, M, K, K, xs)
+    assert np.array_equal(q, q2) and same(d, d2)
+    w = synth.pack_q8(synth.weights(g, N, K))
+    ws = synth.scales(g, N)
+    other = (ws * np.float32(1.5)).astype(np.float32)
+    bias = g.standard_normal(N).astype(np.float32)
+    base = g.standard_normal(M * os_).astype(np.float32)
+    with hip.Q8Matrix(w, ws):
+        for scales, add in ((ws, 1), (other, 0), (other, 1)):
+            want, out = base.copy(), base.copy()
+            ol.gemm_q8(want, os_, w, scales, bias, N, q, d, K, K, M, add, threads=16)
+            say("staging gemm", add, scales is ws)
+            hip.gemm_q8(out, os_, w, scales, bias, N, hip.make_act(q, d, K, K, M), add)
+            assert same(out, want), (add, scales is ws)
+
+
 def test_every_tiling(hip):
     """Every tiling of the per-column product, forced, on shapes that leave
     partial tiles in both directions, odd panel counts, K not a multiple of
