@@ -9,9 +9,15 @@ One hipcc line for gfx950: the kernels (csrc/q8_kernels.hip) and the runtime
                        each (its Makefile builds with the same flag);
   no -ffast-math, no -fgpu-flush-denormals-to-zero: a block's scale can be
                        subnormal, and the division must stay IEEE;
-  -Xclang -target-feature -Xclang -packed-fp32-ops  (disabled: see below)
-The packed-fp32 feature is switched off so the compiler makes no v_pk_*_f32
-from the epilogue's float code.
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                       the packed-fp32 feature off: the compiler makes no
+                       v_pk_*_f32 from the epilogue's float code;
+  -mllvm --amdgpu-mfma-vgpr-form
+                       MFMA accumulators in ordinary VGPRs wherever a kernel
+                       fits them: left to its heuristics the register
+                       allocator splits the accumulators between VGPRs and
+                       AGPRs and copies them around every MFMA of the main
+                       loop (three moves an MFMA in the 128 x 128 tile).
 """
 import os
 import subprocess
@@ -27,6 +33,7 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "--amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-result",
 ]
 

@@ -664,7 +664,11 @@ __device__ __forceinline__ uint32_t lds_addr(const int8_t *p) {
     return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) int8_t *)p);
 }
 
-/* 16 bytes from LDS, issued as written; the caller waits on lgkmcnt */
+/* 16 bytes from LDS, issued as written; the caller waits on lgkmcnt. The
+ * compiler takes the result as ready when the asm ends, so nothing may copy
+ * or reuse the destination before that wait: a kernel whose registers run
+ * out (two fragment sets beside 256 accumulators) gets such copies, and
+ * tests/test_lds_waits.py checks every kernel's assembly for them. */
 __device__ __forceinline__ v4i lds_read16(uint32_t addr) {
     v4i r;
     asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr) : "memory");
@@ -884,6 +888,249 @@ __device__ __forceinline__ void ring_tile(const GemmArgs &g, const Seg &sg, uint
     }
 }
 
+/* ------------------------------------------ the software-pipelined product --
+ *
+ * The same stages and the same LDS DMA as ring_tile, with the fragment reads
+ * moved off the MFMAs' critical path. Every wave holds two fragment sets: the
+ * MFMAs of sub-step g run on one while the ds_reads of sub-step g + 1 fill the
+ * other, so LDS latency and LDS read time hide under the matrix pipe's work.
+ * The barrier that lets a stage's slot be read moves to the start of the
+ * previous stage's last sub-step: by then every wave has read that last
+ * sub-step's fragments (a sub-step ahead), so the slot of stage s is free at
+ * that barrier and takes stage s + NS at once; NS - 1 stages are in flight
+ * while one is multiplied. */
+
+template <int WN, int WM, int TN, int TM, int UPS, int NS, bool PACKED>
+__device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint32_t tn, uint32_t tm) {
+    constexpr int NW = WN * WM;
+    constexpr int BN = 16 * TN * WN, BM = 16 * TM * WM;
+    constexpr int UB = BN / 16, UA = BM / 16, UNITS = UA + UB;
+    constexpr int SLOTU = UNITS * UPS;
+    static_assert(SLOTU % NW == 0, "each wave loads whole units");
+    constexpr int L = SLOTU / NW;
+    static_assert(NS >= 2 && NS <= 4, "two to four slots");
+    static_assert((NS - 1) * L < 64, "the stages in flight fit vmcnt");
+    constexpr int SLOT = SLOTU * kUnitBytes;
+    static_assert(NS * SLOT <= 160 * 1024, "the slots fit a CU's LDS");
+    static_assert((UPS & (UPS - 1)) == 0, "a power of two units a stage");
+    static_assert(NS * UPS % 2 == 0, "the steady state is whole pairs of sub-steps");
+    constexpr int R = TN + TM;
+    __shared__ __attribute__((aligned(1024))) int8_t ring[NS * SLOT];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wn = wave % WN, wm = wave / WN;
+    const uint32_t T = sg.T;
+    const uint32_t n0 = tn * BN, m0 = tm * BM;
+    const uint32_t npan = g.rows >> 4;
+    const uint32_t n = g.n, ns = g.ku / UPS;
+
+    if (g.rmode)
+        __builtin_amdgcn_s_setreg(2049, g.rmode);    /* MODE.FP_ROUND, single precision */
+
+    const int8_t *src[L];
+    bool isw[L];
+    uint32_t sub[L];
+#pragma unroll
+    for (int s = 0; s < L; s++) {
+        const int idx = wave * L + s, kk = idx / UNITS, u = idx % UNITS;
+        sub[s] = kk;
+        if (u < UB) {
+            uint32_t p = n0 / 16 + u;
+            p = p < npan ? p : npan - 1;
+            src[s] = g.w + (size_t)p * kUnitBytes + lane * 16;
+            isw[s] = true;
+        } else if (PACKED) {
+            const uint32_t ng = (T + 15) / 16;
+            uint32_t gi = m0 / 16 + (u - UB);
+            gi = gi < ng ? gi : ng - 1;
+            src[s] = sg.q + (size_t)gi * kUnitBytes + lane * 16;
+            isw[s] = false;
+        } else {
+            uint32_t row = m0 + (u - UB) * 16 + (lane & 15);
+            row = row < T ? row : T - 1;
+            src[s] = sg.q + (size_t)row * n;
+            isw[s] = false;
+        }
+    }
+    auto issue = [&](uint32_t j) {
+        int8_t *slot = ring + (j % NS) * SLOT;
+#pragma unroll
+        for (int s = 0; s < L; s++) {
+            const uint32_t unit = j * UPS + sub[s];
+            const int8_t *gp;
+            if (isw[s]) {
+                gp = src[s] + (size_t)unit * g.wstride;
+            } else if (PACKED) {
+                gp = src[s] + (size_t)unit * sg.qstride;
+            } else {
+                const uint32_t k = unit * 64 + (lane >> 4) * 16;
+                gp = src[s] + (k < n ? k : 0);
+            }
+            __builtin_amdgcn_global_load_lds(PK_AS1(gp), PK_AS3(slot + (wave * L + s) * kUnitBytes), 16, 0, 0);
+        }
+    };
+
+    v4i acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; i++)
+#pragma unroll
+        for (int j = 0; j < TM; j++)
+            acc[i][j] = v4i{0, 0, 0, 0};
+
+    const uint32_t wbase = lds_addr(ring) + (wn * TN) * kUnitBytes + lane * 16;
+    const uint32_t abase = lds_addr(ring) + (UB + wm * TM) * kUnitBytes + lane * 16;
+    /* LDS offset of sub-step gi's fragments */
+    auto at_of = [&](uint32_t gi) {
+        const uint32_t s = gi / UPS, kk = gi % UPS;
+        return (s % NS) * SLOT + kk * UNITS * kUnitBytes;
+    };
+    auto read_set = [&](v4i (&f)[R], uint32_t at) {
+#pragma unroll
+        for (int i = 0; i < TN; i++)
+            f[i] = lds_read16(wbase + at + i * kUnitBytes);
+#pragma unroll
+        for (int j = 0; j < TM; j++)
+            f[TN + j] = lds_read16(abase + at + j * kUnitBytes);
+    };
+    /* Sub-step gi multiplies the fragments read a sub-step ago (cur) and
+     * reads gi + 1's (nxt). At the last sub-step of stage s < ns - 1 the
+     * workgroup first waits for stage s + 1 (LATER stages of this thread's
+     * loads may stay in flight) and meets, and with ISSUE refills stage s's
+     * slot with stage s + NS. Every choice is a template argument, so the
+     * loop below has no branch but its own and the accumulators stay put. */
+    auto step = [&](uint32_t gi, auto barrier, auto later, auto refill, auto more, v4i (&cur)[R],
+                    v4i (&nxt)[R]) {
+        wait_lgkm<0>();
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            asm volatile("" : "+v"(cur[r]));
+        if constexpr (decltype(barrier)::value) {
+            wait_vm<decltype(later)::value * L>();
+            __builtin_amdgcn_s_barrier();
+            if constexpr (decltype(refill)::value)
+                issue(gi / UPS + NS);
+        }
+        if constexpr (decltype(more)::value)
+            read_set(nxt, at_of(gi + 1));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TN; i++)
+#pragma unroll
+            for (int j = 0; j < TM; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur[i], cur[TN + j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    v4i f0[R], f1[R];
+    auto setpair = [&](auto k) -> auto & {
+        if constexpr (decltype(k)::value % 2 == 0) return f0; else return f1;
+    };
+
+    /* The epilogue's per-frame scales and per-channel scales and biases,
+     * staged into LDS ahead of stage 0: the oldest loads of each wave, so
+     * the wait for stage 0 covers them, and the epilogue finds them in LDS
+     * instead of waiting a memory round trip after the last MFMA. Each
+     * segment is whole 64-float chunks; indexes past the tile's frames or
+     * channels read the last one (their results are never stored). */
+    constexpr int ED = (BM + 63) / 64, EW = (BN + 63) / 64, ECH = ED + 2 * EW;
+    __shared__ __attribute__((aligned(256))) float epi[ECH * 64];
+    {
+        const int nch = g.bias ? ECH : ED + EW;
+        for (int c = wave; c < nch; c += NW) {
+            const float *a;
+            if (c < ED) {
+                const uint32_t t = m0 + c * 64 + lane;
+                a = sg.d + (t < T ? t : T - 1);
+            } else {
+                const uint32_t r = n0 + ((c - ED) % EW) * 64 + lane;
+                a = (c < ED + EW ? g.ws : g.bias) + (r < g.rows ? r : g.rows - 1);
+            }
+            __builtin_amdgcn_global_load_lds(PK_AS1(a), PK_AS3(epi + c * 64), 4, 0, 0);
+        }
+    }
+
+    /* the caller guarantees ns >= NS */
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+        issue(j);
+    wait_vm<(NS - 1) * L>();
+    __builtin_amdgcn_s_barrier();
+    read_set(f0, 0);
+
+    /* steady state: stages [0, ns - NS), each refilling its slot; SPI
+     * sub-steps a pass, an even number, so f0 and f1 alternate statically */
+    constexpr int SPI = UPS > 2 ? UPS : 2;
+    const uint32_t steady = (ns - NS) * UPS;
+    for (uint32_t gi = 0; gi < steady; gi += SPI) {
+        for_static<0, SPI>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            constexpr bool bar = k % UPS == UPS - 1;
+            step(gi + k, std::integral_constant<bool, bar>{}, std::integral_constant<int, NS - 2>{},
+                 std::integral_constant<bool, bar>{}, yes{}, setpair(std::integral_constant<int, k>{}),
+                 setpair(std::integral_constant<int, k + 1>{}));
+        });
+    }
+    /* drain: stages ns - NS .. ns - 2, loading nothing more; then the last */
+    for_static<0, NS * UPS>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        constexpr int b = k / UPS;                        /* stage ns - NS + b */
+        constexpr bool bar = k % UPS == UPS - 1 && b < NS - 1;
+        constexpr int later = NS - 2 - b < 0 ? 0 : NS - 2 - b;
+        constexpr bool more = k + 1 < NS * UPS;
+        step(steady + k, std::integral_constant<bool, bar>{}, std::integral_constant<int, later>{}, no{},
+             std::integral_constant<bool, more>{}, setpair(std::integral_constant<int, k>{}),
+             setpair(std::integral_constant<int, k + 1>{}));
+    });
+    wait_vm<0>();
+
+    const bool vec = ((sg.os & 3) == 0) && ((((uintptr_t)sg.out) & 15) == 0);
+#pragma unroll
+    for (int j = 0; j < TM; j++) {
+        const uint32_t t = m0 + (wm * TM + j) * 16 + (lane & 15);
+        if (t >= T)
+            continue;
+        const float dt = epi[t - m0];
+#pragma unroll
+        for (int i = 0; i < TN; i++) {
+            const uint32_t c = n0 + (wn * TN + i) * 16 + (lane >> 4) * 4;
+            if (c >= g.rows)
+                continue;
+            const float4 wsv = *(const float4 *)&epi[ED * 64 + (c - n0)];
+            const float wsr[4] = { wsv.x, wsv.y, wsv.z, wsv.w };
+            float bsr[4] = { 0, 0, 0, 0 };
+            if (g.bias) {
+                const float4 bv = *(const float4 *)&epi[(ED + EW) * 64 + (c - n0)];
+                bsr[0] = bv.x; bsr[1] = bv.y; bsr[2] = bv.z; bsr[3] = bv.w;
+            }
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                v[r] = __builtin_fmaf((float)acc[i][j][r], dt, 0.0f) * wsr[r];
+                if (g.bias)
+                    v[r] = v[r] + bsr[r];
+            }
+            float *o = sg.out + (size_t)t * sg.os + c;
+            if (vec) {
+                float4 ov = make_float4(v[0], v[1], v[2], v[3]);
+                if (g.add) {
+                    const float4 old = *(const float4 *)o;
+                    ov.x = old.x + ov.x;
+                    ov.y = old.y + ov.y;
+                    ov.z = old.z + ov.z;
+                    ov.w = old.w + ov.w;
+                }
+                *(float4 *)o = ov;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    o[r] = g.add ? o[r] + v[r] : v[r];
+            }
+        }
+    }
+}
+
 /* The hardware deals workgroup b to XCD b % 8. Renumbered so that each XCD
  * takes a contiguous run of tiles, and the run ordered in groups of 8 frame
  * tiles by every channel tile, the workgroups one XCD runs at once share
@@ -944,28 +1191,71 @@ static void run_ring(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
         run_ring1<WN, WM, TN, TM, UPS, false>(g, tab, s);
 }
 
+template <int WN, int WM, int TN, int TM, int UPS, int NS, bool PACKED>
+__global__ __launch_bounds__(64 * WN * WM) void gemm_pipe_kernel(GemmArgs g, Seg sg, uint32_t tiles_n,
+                                                                 uint32_t tiles_m) {
+    uint32_t tn, tm;
+    xcd_tile(blockIdx.x, gridDim.x, tiles_n, tiles_m, tn, tm);
+    pipe_tile<WN, WM, TN, TM, UPS, NS, PACKED>(g, sg, tn, tm);
+}
+
+template <int WN, int WM, int TN, int TM, int UPS, int NS, bool PACKED>
+__global__ __launch_bounds__(64 * WN * WM) void gemm_pipe_grouped_kernel(GemmArgs g, SegTable tab,
+                                                                         uint32_t tiles_n) {
+    const uint32_t tm = blockIdx.x / tiles_n;
+    uint32_t i = 0;
+    while (i + 1 < tab.nseg && tab.s[i + 1].tile0 <= tm)
+        i++;
+    pipe_tile<WN, WM, TN, TM, UPS, NS, PACKED>(g, tab.s[i], blockIdx.x % tiles_n, tm - tab.s[i].tile0);
+}
+
+template <int WN, int WM, int TN, int TM, int UPS, int NS, bool PACKED>
+static void run_pipe1(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
+    constexpr uint32_t BN = 16 * TN * WN, BM = 16 * TM * WM;
+    constexpr uint32_t threads = 64 * WN * WM;
+    const uint32_t tiles_n = (g.rows + BN - 1) / BN;
+    if (tab.nseg == 1) {
+        const uint32_t tiles_m = (tab.s[0].T + BM - 1) / BM;
+        gemm_pipe_kernel<WN, WM, TN, TM, UPS, NS, PACKED><<<tiles_n * tiles_m, threads, 0, s>>>(g, tab.s[0], tiles_n, tiles_m);
+    } else {
+        SegTable t = tab;
+        uint32_t tiles = 0;
+        for (uint32_t i = 0; i < t.nseg; i++) {
+            t.s[i].tile0 = tiles;
+            tiles += (t.s[i].T + BM - 1) / BM;
+        }
+        gemm_pipe_grouped_kernel<WN, WM, TN, TM, UPS, NS, PACKED><<<tiles_n * tiles, threads, 0, s>>>(g, t, tiles_n);
+    }
+}
+
+template <int WN, int WM, int TN, int TM, int UPS, int NS>
+static void run_pipe(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
+    if (tab.s[0].qstride)
+        run_pipe1<WN, WM, TN, TM, UPS, NS, true>(g, tab, s);
+    else
+        run_pipe1<WN, WM, TN, TM, UPS, NS, false>(g, tab, s);
+}
+
 /* The pipelined product's tile shapes: channels x frames, and the units of
  * inputs a stage (ku must divide into four stages of them). */
 struct RingCfg {
     const char *name;
     uint32_t bn, bm, ups;
+    uint32_t slots;                 /* 0: ring_tile (four slots, four-stage passes) */
     void (*run)(const GemmArgs &, const SegTable &, hipStream_t);
 };
 static const RingCfg kRing[] = {
-    { "ring<128x128,1>", 128, 128, 1, run_ring<2, 2, 4, 4, 1> },
-    { "ring<128x128,2>", 128, 128, 2, run_ring<2, 2, 4, 4, 2> },
-    { "ring<64x64,1>", 64, 64, 1, run_ring<2, 2, 2, 2, 1> },
-    { "ring<64x64,2>", 64, 64, 2, run_ring<2, 2, 2, 2, 2> },
-    { "ring<64x64,4>", 64, 64, 4, run_ring<2, 2, 2, 2, 4> },
-    { "ring<128x64,2>", 128, 64, 2, run_ring<4, 1, 2, 4, 2> },
-    { "ring<256x128,1>", 256, 128, 1, run_ring<4, 2, 4, 4, 1> },
-    { "ring<128x256,1>", 128, 256, 1, run_ring<2, 4, 4, 4, 1> },
-    { "ring<64x128,2>", 64, 128, 2, run_ring<2, 2, 2, 4, 2> },
-    { "ring<256x256,1>", 256, 256, 1, run_ring<2, 2, 8, 8, 1> },
-    { "ring<256x256w8,1>", 256, 256, 1, run_ring<2, 4, 8, 4, 1> },
-    { "ring<256x128w4,1>", 256, 128, 1, run_ring<2, 2, 8, 4, 1> },
-    { "ring<128x256w4,1>", 128, 256, 1, run_ring<2, 2, 4, 8, 1> },
-    { "ring<128x256w8,1>", 128, 256, 1, run_ring<2, 4, 4, 4, 1> },
+    /* ring_tile: name <channels x frames, units a stage> */
+    { "ring<128x128,1>", 128, 128, 1, 0, run_ring<2, 2, 4, 4, 1> },
+    { "ring<64x64,1>", 64, 64, 1, 0, run_ring<2, 2, 2, 2, 1> },
+    { "ring<64x64,2>", 64, 64, 2, 0, run_ring<2, 2, 2, 2, 2> },
+    { "ring<64x64,4>", 64, 64, 4, 0, run_ring<2, 2, 2, 2, 4> },
+    /* pipe_tile: name <channels x frames, units a stage, slots>; w8: eight
+     * waves of 64 x 32 */
+    { "pipe<128x128,1,4>", 128, 128, 1, 4, run_pipe<2, 2, 4, 4, 1, 4> },
+    { "pipe<128x128w8,1,4>", 128, 128, 1, 4, run_pipe<2, 4, 4, 2, 1, 4> },
+    { "pipe<64x64,2,4>", 64, 64, 2, 4, run_pipe<2, 2, 2, 2, 2, 4> },
+    { "pipe<64x64,4,4>", 64, 64, 4, 4, run_pipe<2, 2, 2, 2, 4, 4> },
 };
 constexpr int kNRing = sizeof kRing / sizeof kRing[0];
 
@@ -982,22 +1272,34 @@ int ring_count() { return kNRing; }
 
 /* The tile for a product of `frames` frames into `rows` channels: the
  * largest that still gives every CU a workgroup. */
+/* whether tiling i takes ku units a panel: ring_tile runs whole passes of
+ * four stages; pipe_tile needs its slots' worth of stages to start */
+static bool fits(int i, uint32_t ku) {
+    const RingCfg &c = kRing[i];
+    if (c.slots == 0)
+        return ku % (4 * c.ups) == 0;
+    return ku % c.ups == 0 && ku / c.ups >= c.slots;
+}
+
 static int pick_ring(uint32_t rows, uint64_t frames, uint32_t ku) {
-    if (g_forced_ring >= 0 && ku % (4 * kRing[g_forced_ring].ups) == 0)
+    if (g_forced_ring >= 0 && fits(g_forced_ring, ku))
         return g_forced_ring;
     auto tiles = [&](int i) { return (uint64_t)((rows + kRing[i].bn - 1) / kRing[i].bn) * ((frames + kRing[i].bm - 1) / kRing[i].bm); };
-    /* measured on the layer's shapes at 750 and 7500 frames: deep inputs
-     * (K >= 2048) with a CU's worth of 128 x 128 tiles take those; otherwise
-     * 64 x 64 tiles, with longer stages the fewer the tiles (more of a
-     * workgroup's loads in flight where workgroups are few) */
-    if (ku >= 32 && tiles(0) >= 256)
-        return 0;
-    const uint64_t t64 = tiles(2);
+    /* measured on the layer's shapes at 750 and 7500 frames (every tiling,
+     * every product): a CU's worth of 128 x 128 tiles takes the eight-wave
+     * pipelined tile; fewer take 64 x 64 pipelined tiles of two-unit stages;
+     * inputs too short for their slots take the ring, 64 x 64, with longer
+     * stages the fewer the tiles */
+    if (tiles(0) >= 256 && fits(5, ku))
+        return 5;
+    if (fits(6, ku))
+        return 6;
+    const uint64_t t64 = tiles(1);
     if (t64 >= 512)
-        return 2;
+        return 1;
     if (t64 >= 256 && ku % 8 == 0)
-        return 3;
-    return ku % 16 == 0 ? 4 : ku % 8 == 0 ? 3 : 2;
+        return 2;
+    return ku % 16 == 0 ? 3 : ku % 8 == 0 ? 2 : 1;
 }
 
 template <int WN, int WM, int TN, int TM, int MODE>
