@@ -11,8 +11,11 @@ to int8 and multiplied with exact int32 sums into fp32 outputs by the
 reference's epilogue. Weights, scales and fp32 inputs are synthetic (int8
 uniform [-127, 127], scales uniform [1e-3, 1e-2], N(0, 1) inputs, half-normal
 into the down projections) and resident in HBM before the timed region. The
-22 launches of a step are captured once into a HIP graph and replayed; K
-replays are timed with events on the stream they run on.
+16 launches of a step (8 quantizes, 7 products, and one launch of the
+attention's q, k, v and positions' products, which the reference runs from
+one activation and the positional encodings) are captured once into a HIP
+graph and replayed; K replays are timed with events on the stream they run
+on.
 
 Printed: one JSON line. `value` is TOPS (2 M K N over the step's time). The
 `extra` object adds the long-form layer (M = 7500) and a ragged batch of 8
@@ -185,9 +188,30 @@ def kernel_ms(pk, torch, prod, launches=64, reps=5, packed=True):
 
 # ------------------------------------------------------------ workloads ---
 
-def layer_step(pk, prods, packed=True):
+ATTENTION = ("q", "k", "v", "pos")
+
+
+def batch_gemm(pk, group, stream=None):
+    """The attention's independent products (q, k, v of one activation and the
+    positions' projection) in one launch."""
+    pk.gemm_q8_batch_dev([(p.out, p.N, p.m, 0, p.N, p.m.dev_scales, None, p.qp, p.d, p.K, p.M, p.add)
+                          for p in group], stream=stream)
+
+
+def layer_step(pk, prods, packed=True, batch=True):
+    """One layer's quantizes and products in the reference's order; with batch,
+    q, k, v and pos go to one launch after q's quantize."""
+    group = [p for p in prods if p.name in ATTENTION] if batch and packed else []
+
     def fn():
         for p in prods:
+            if group and p.name in ATTENTION:
+                if p is group[0]:
+                    for a in group:
+                        if a.quantizes:
+                            a.quantize(pk)
+                    batch_gemm(pk, group)
+                continue
             if p.quantizes:
                 p.quantize(pk, packed=packed)
             p.gemm(pk, packed=packed)
@@ -217,9 +241,11 @@ def check_replay(pk, torch, prods, graph):
 def encoder_sweep(pk, torch, M, seed):
     """24 layers with independent weights (~0.6 GB of int8 in HBM),
     each product's input the previous product's fp32 output re-quantized per
-    row, in the order ff1_up, ff1_down, q, k, v, o, pw1 (first 1024 of its 2048
-    columns into pw2), pw2, ff2_up, ff2_down; the positions' projection reads
-    the positional encodings, quantized once an encode as the reference does.
+    row, in the order ff1_up, ff1_down, q (k and v multiply q's activation and
+    go to one launch with the positions' projection), o (on v's output), pw1
+    (first 1024 of its 2048 columns into pw2), pw2, ff2_up, ff2_down; the
+    positions' projection reads the positional encodings, quantized once an
+    encode as the reference does.
     Each matrix's scales are the configs' uniform [1e-3, 1e-2] times
     1 / (sqrt(K) * 73.6 * 0.0055) so that a chain of 264 products keeps its
     activations finite (timing does not depend on the values)."""
@@ -242,8 +268,11 @@ def encoder_sweep(pk, torch, M, seed):
         for name in order:
             _, mm, K, N, half, add = shapes[name]
             p = Product(pk, torch, name, mm, K, N, half, add, g, x_dev=prev, xs=prev_xs, ws_gain=gain(K))
+            if name in ("k", "v"):
+                p.share(lay["q"])           # one activation for q, k and v, as the reference has
             lay[name] = p
-            prev, prev_xs = p.out, N
+            if name not in ("q", "k"):
+                prev, prev_xs = p.out, N
         _, mm, K, N, half, add = shapes["pos"]
         pp = Product(pk, torch, "pos", mm, K, N, half, add, g, x_dev=ape, xs=1024, ws_gain=gain(K))
         pp.q, pp.d, pp.qp = ape_q, ape_d, ape_qp
@@ -255,10 +284,11 @@ def encoder_sweep(pk, torch, M, seed):
     def fn():
         pk.quantize_packed_dev(ape_q, ape_qp, ape_d, ape, 1024, 2 * M - 1, 1024)
         for lay in layers:
-            for name in order[:5]:
+            for name in order[:2]:
                 lay[name].quantize(pk)
                 lay[name].gemm(pk)
-            lay["pos"].gemm(pk)
+            lay["q"].quantize(pk)
+            batch_gemm(pk, [lay[n] for n in ATTENTION])
             for name in order[5:]:
                 p = lay[name]
                 p.quantize(pk)

@@ -165,6 +165,28 @@ int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, c
                                const float *bias, const pk_hip_seg *segs, uint32_t nseg, int add,
                                void *stream);
 
+/* One product of a batch: an uploaded matrix's run of panels [r0, r0 + rows)
+ * with its scales and bias at r0 (device), the packed per-row activations qp
+ * of a (a->q is not read), and the outputs out[t * os + r]. */
+typedef struct {
+    float             *out;
+    size_t             os;
+    const pk_hip_q8   *m;
+    uint32_t           r0, rows;
+    const float       *ws, *bias;
+    pk_hip_act         a;
+    const int8_t      *qp;
+    int                add;
+} pk_hip_job;
+
+/* njobs <= 8 independent products in one launch, each job's outputs the bits
+ * pk_hip_gemm_q8_packed_dev gives it alone. The reference runs such products
+ * one after another (core/encoder.c:329-368: the attention's q, k and v of one
+ * activation, and the positions' projection); a device-resident caller
+ * launches them together. The jobs share n and per-row blocks (qb == n);
+ * device pointers throughout. */
+int pk_hip_gemm_q8_batch_dev(const pk_hip_job *jobs, uint32_t njobs, int rmode, void *stream);
+
 /* The kernel variant the calling thread launched last, for profiling and
  * tests. */
 const char *pk_hip_last_kernel(void);

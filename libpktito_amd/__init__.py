@@ -50,6 +50,13 @@ class Seg(ctypes.Structure):
     _fields_ = [("out", ctypes.c_void_p), ("os", ctypes.c_size_t), ("a", Act)]
 
 
+class Job(ctypes.Structure):
+    """pk_hip_job: one product of a batch."""
+    _fields_ = [("out", ctypes.c_void_p), ("os", ctypes.c_size_t), ("m", ctypes.c_void_p),
+                ("r0", ctypes.c_uint32), ("rows", ctypes.c_uint32), ("ws", ctypes.c_void_p),
+                ("bias", ctypes.c_void_p), ("a", Act), ("qp", ctypes.c_void_p), ("add", ctypes.c_int)]
+
+
 _lib = None
 
 # every function include/pk_hip.h declares, with its ctypes signature
@@ -84,6 +91,8 @@ _SIGS = {
     "pk_hip_gemm_q8_grouped_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                   ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(Seg),
                                                   ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]),
+    "pk_hip_gemm_q8_batch_dev": (ctypes.c_int, [ctypes.POINTER(Job), ctypes.c_uint32, ctypes.c_int,
+                                                ctypes.c_void_p]),
 }
 
 
@@ -256,3 +265,14 @@ def gemm_q8_grouped_dev(m, r0, rows, ws_ptr, bias, segs, add, stream=None):
         arr[i] = Seg(_dptr(out), os_, Act(_dptr(q), _dptr(d), n, qb, T))
     _check(lib().pk_hip_gemm_q8_grouped_dev(m.handle, r0, rows, ws_ptr, _dptr(bias), arr, len(segs),
                                             int(add), _stream(stream)))
+
+
+def gemm_q8_batch_dev(jobs, rmode=0, stream=None):
+    """Independent products in one launch: jobs [(out, os, m, r0, rows, ws_ptr,
+    bias, qp, d, n, T, add), ...] of device tensors, m a Q8Matrix, qp packed
+    per-row activations."""
+    arr = (Job * len(jobs))()
+    for i, (out, os_, m, r0, rows, ws_ptr, bias, qp, d, n, T, add) in enumerate(jobs):
+        arr[i] = Job(_dptr(out), os_, m.handle, r0, rows, ws_ptr, _dptr(bias), Act(None, _dptr(d), n, n, T),
+                     _dptr(qp), int(add))
+    _check(lib().pk_hip_gemm_q8_batch_dev(arr, len(jobs), int(rmode), _stream(stream)))

@@ -647,6 +647,57 @@ int pk_hip_gemm_q8_packed_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_
     return launch_product(out, os, m, r0, rows, ws, bias, a, add, rmode, (hipStream_t)stream, qp);
 }
 
+int pk_hip_gemm_q8_batch_dev(const pk_hip_job *jobs, uint32_t njobs, int rmode, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!jobs || njobs == 0 || njobs > (uint32_t)pkq8::kMaxJobs)
+        return fail(PK_HIP_EINVAL, "gemm_q8_batch_dev: njobs %u is not in [1, %d]", njobs, pkq8::kMaxJobs);
+    if (rmode < 0 || rmode > 3)
+        return fail(PK_HIP_EROUND, "gemm_q8_batch_dev: rmode %d", rmode);
+    pkq8::JobTable tab;
+    tab.njobs = njobs;
+    const uint32_t n = jobs[0].a.n;
+    for (uint32_t j = 0; j < njobs; j++) {
+        const pk_hip_job &jb = jobs[j];
+        const pk_hip_act *a = &jb.a;
+        if (!jb.m)
+            return fail(PK_HIP_ENOTUP, "gemm_q8_batch_dev: job %u has no matrix", j);
+        if (a->n != n || a->qb != n || n % 32 || n > 16384)
+            return fail(PK_HIP_EINVAL, "gemm_q8_batch_dev: job %u has n %u qb %u; the jobs share n and qb == n",
+                        j, a->n, a->qb);
+        if (a->T && (!a->d || !jb.qp || ((uintptr_t)jb.qp & 15) || !jb.out || !jb.ws))
+            return fail(PK_HIP_EINVAL, "gemm_q8_batch_dev: job %u needs out, ws, d and a 16-byte aligned qp", j);
+        if (a->T > 1 && jb.os < jb.rows)
+            return fail(PK_HIP_EINVAL, "gemm_q8_batch_dev: job %u output stride %zu is under rows %u", j, jb.os,
+                        jb.rows);
+        if ((e = check_panel(jb.m, jb.r0, jb.rows, n)))
+            return e;
+        if (jb.m->ku != jobs[0].m->ku)
+            return fail(PK_HIP_EINVAL, "gemm_q8_batch_dev: job %u's matrix is padded to other units", j);
+        pkq8::GemmArgs &g = tab.g[j];
+        g.w = jb.m->w + (size_t)(jb.r0 / 16) * pkq8::kUnitBytes;
+        g.wstride = (uint64_t)(jb.m->rows / 16) * pkq8::kUnitBytes;
+        g.ws = jb.ws;
+        g.bias = jb.bias;
+        g.rows = jb.rows;
+        g.n = n;
+        g.ku = jb.m->ku;
+        g.kr = pkq8::units_with_data(jb.m->cols);
+        g.qb = n;
+        g.nb = 1;
+        g.add = jb.add;
+        g.rmode = rmode;
+        tab.s[j] = pkq8::Seg{ jb.out, jb.qp, a->d, (uint64_t)jb.os,
+                              (uint64_t)pkq8::packed_groups(a->T) * pkq8::kUnitBytes, a->T, 0 };
+    }
+    const char *name = "";
+    if (pkq8::launch_gemm_batch(tab, (hipStream_t)stream, &name))
+        return hip_fail(hipGetLastError(), "gemm_q8_batch_dev launch");
+    g_kernel = name;
+    return PK_HIP_OK;
+}
+
 int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, const float *ws,
                                const float *bias, const pk_hip_seg *segs, uint32_t nseg, int add,
                                void *stream) {

@@ -87,6 +87,24 @@ int set_ring(int i);
 /* One product; table->nseg == 1 for a plain call. */
 int launch_gemm(const GemmArgs &g, const SegTable &table, hipStream_t s, const char **name);
 
+/* Independent products in one launch: job j is the product g[j] x s[j] (one
+ * segment each). All share n, ku, per-row blocks, packed activations and the
+ * rounding mode. Its workgroups start at wg0[j], a multiple of 8, so every
+ * job's first tile runs on XCD 0 and the XCD-aware tile order holds inside
+ * each job; the workgroups between one job's tiles and the next job's start
+ * do nothing. */
+constexpr int kMaxJobs = 8;
+
+struct JobTable {
+    GemmArgs g[kMaxJobs];
+    Seg s[kMaxJobs];
+    uint32_t wg0[kMaxJobs + 1];
+    uint32_t tiles_n[kMaxJobs], tiles[kMaxJobs];
+    uint32_t njobs;
+};
+
+int launch_gemm_batch(const JobTable &jobs, hipStream_t s, const char **name);
+
 }  // namespace pkq8
 
 #endif

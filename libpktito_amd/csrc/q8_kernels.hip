@@ -50,6 +50,28 @@ __device__ __forceinline__ bool zero_block(float amax, int nan) {
     return nan || !__builtin_isfinite(amax) || amax < 0x1p-121f;
 }
 
+/* The same block rule on magnitude bits: m = the largest (bits & 0x7fffffff)
+ * of the block. Non-negative floats order as their bit patterns do, NaN above
+ * infinity above every finite value, so the block holds a NaN or an infinity
+ * exactly when m >= 0x7f800000, and otherwise m is the bits of amax; 2^-121
+ * is 0x03000000. */
+__device__ __forceinline__ bool zero_bits(uint32_t m) { return m >= 0x7f800000u || m < 0x03000000u; }
+
+__device__ __forceinline__ int mag_bits(float v) { return (int)(__float_as_uint(v) & 0x7fffffffu); }
+
+/* The maximum over the wave of a non-negative int, in every lane: DPP within
+ * rows of 16 lanes (quad swaps, half mirror, mirror), the row broadcasts
+ * across rows, then lane 63's value. All 64 lanes must be active. */
+__device__ __forceinline__ int wave_max_nonneg(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));    /* quad_perm 1,0,3,2 */
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));    /* quad_perm 2,3,0,1 */
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));   /* row_half_mirror */
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));   /* row_mirror */
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false));   /* row_bcast15: rows 1, 3 */
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false));   /* row_bcast31: rows 2, 3 */
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 /* A whole column is one block (qb == n, "per-row" quantization): one
  * workgroup of W waves a column, each thread up to CH chunks of 16 inputs,
  * held in registers between the max and the rounding. */
@@ -201,24 +223,20 @@ __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q,
     const uint32_t n4 = n >> 2;
     const float4 *xr = (const float4 *)(x + (size_t)t * xs);
     float4 v[CH];
-    float amax = 0.0f;
-    int nan = 0;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
         v[c] = i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+    int m = 0;
 #pragma unroll
     for (int c = 0; c < CH; c++)
-        absmax4(v[c], amax, nan);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-        nan |= __shfl_xor(nan, off, 64);
-    }
-    const bool zero = zero_block(amax, nan);
+        m = max(max(max(m, mag_bits(v[c].x)), max(mag_bits(v[c].y), mag_bits(v[c].z))), mag_bits(v[c].w));
+    const uint32_t mb = (uint32_t)wave_max_nonneg(m);
+    const bool zero = zero_bits(mb);
     float dv = 0.0f, id = 0.0f;
     if (!zero) {
+        const float amax = __uint_as_float(mb);
         dv = amax / 127.0f;
         id = 127.0f / amax;
     }
@@ -900,30 +918,35 @@ __device__ __forceinline__ void ring_tile(const GemmArgs &g, const Seg &sg, uint
  * that barrier and takes stage s + NS at once; NS - 1 stages are in flight
  * while one is multiplied. */
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, bool PACKED>
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED>
 __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint32_t tn, uint32_t tm) {
-    constexpr int NW = WN * WM;
+    constexpr int NW = WN * WM;             /* waves of one K group */
     constexpr int BN = 16 * TN * WN, BM = 16 * TM * WM;
     constexpr int UB = BN / 16, UA = BM / 16, UNITS = UA + UB;
     constexpr int SLOTU = UNITS * UPS;
     static_assert(SLOTU % NW == 0, "each wave loads whole units");
     constexpr int L = SLOTU / NW;
-    static_assert(NS >= 2 && NS <= 4, "two to four slots");
+    static_assert(NS >= 2 && NS <= 8, "two to eight slots");
     static_assert((NS - 1) * L < 64, "the stages in flight fit vmcnt");
     constexpr int SLOT = SLOTU * kUnitBytes;
-    static_assert(NS * SLOT <= 160 * 1024, "the slots fit a CU's LDS");
+    static_assert(KG * NS * SLOT <= 160 * 1024, "the slots fit a CU's LDS");
+    static_assert(KG == 1 || (KG - 1) * NW * TN * TM * kUnitBytes <= NS * SLOT, "the partial sums fit a ring");
     static_assert((UPS & (UPS - 1)) == 0, "a power of two units a stage");
     static_assert(NS * UPS % 2 == 0, "the steady state is whole pairs of sub-steps");
     constexpr int R = TN + TM;
-    __shared__ __attribute__((aligned(1024))) int8_t ring[NS * SLOT];
+    __shared__ __attribute__((aligned(1024))) int8_t rings[KG * NS * SLOT];
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    /* K group kg takes units [kg ku / KG, (kg + 1) ku / KG) with a ring of its
+     * own; its NW waves tile the workgroup's outputs as a whole group would */
+    const int kg = wv / NW, wave = wv % NW;
     const int wn = wave % WN, wm = wave / WN;
+    int8_t *const ring = rings + kg * NS * SLOT;
     const uint32_t T = sg.T;
     const uint32_t n0 = tn * BN, m0 = tm * BM;
     const uint32_t npan = g.rows >> 4;
-    const uint32_t n = g.n, ns = g.ku / UPS;
+    const uint32_t n = g.n, kug = g.ku / KG, u0 = kg * kug, ns = kug / UPS;
 
     if (g.rmode)
         __builtin_amdgcn_s_setreg(2049, g.rmode);    /* MODE.FP_ROUND, single precision */
@@ -957,7 +980,7 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
         int8_t *slot = ring + (j % NS) * SLOT;
 #pragma unroll
         for (int s = 0; s < L; s++) {
-            const uint32_t unit = j * UPS + sub[s];
+            const uint32_t unit = u0 + j * UPS + sub[s];
             const int8_t *gp;
             if (isw[s]) {
                 gp = src[s] + (size_t)unit * g.wstride;
@@ -1036,7 +1059,7 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
      * channels read the last one (their results are never stored). */
     constexpr int ED = (BM + 63) / 64, EW = (BN + 63) / 64, ECH = ED + 2 * EW;
     __shared__ __attribute__((aligned(256))) float epi[ECH * 64];
-    {
+    if (kg == 0) {
         const int nch = g.bias ? ECH : ED + EW;
         for (int c = wave; c < nch; c += NW) {
             const float *a;
@@ -1084,6 +1107,30 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
              setpair(std::integral_constant<int, k + 1>{}));
     });
     wait_vm<0>();
+
+    if constexpr (KG > 1) {
+        /* every wave is done reading its ring: the other groups hand their
+         * int32 sums to group 0 through LDS (exact in any order) */
+        __builtin_amdgcn_s_barrier();
+        v4i *xch = (v4i *)rings;
+        if (kg > 0) {
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+#pragma unroll
+                for (int j = 0; j < TM; j++)
+                    xch[(((kg - 1) * NW + wave) * TN * TM + i * TM + j) * 64 + lane] = acc[i][j];
+        }
+        __syncthreads();
+        if (kg > 0)
+            return;
+#pragma unroll
+        for (int h = 1; h < KG; h++)
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+#pragma unroll
+                for (int j = 0; j < TM; j++)
+                    acc[i][j] += xch[(((h - 1) * NW + wave) * TN * TM + i * TM + j) * 64 + lane];
+    }
 
     const bool vec = ((sg.os & 3) == 0) && ((((uintptr_t)sg.out) & 15) == 0);
 #pragma unroll
@@ -1191,32 +1238,32 @@ static void run_ring(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
         run_ring1<WN, WM, TN, TM, UPS, false>(g, tab, s);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, bool PACKED>
-__global__ __launch_bounds__(64 * WN * WM) void gemm_pipe_kernel(GemmArgs g, Seg sg, uint32_t tiles_n,
-                                                                 uint32_t tiles_m) {
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED>
+__global__ __launch_bounds__(64 * WN * WM * KG) void gemm_pipe_kernel(GemmArgs g, Seg sg, uint32_t tiles_n,
+                                                                      uint32_t tiles_m) {
     uint32_t tn, tm;
     xcd_tile(blockIdx.x, gridDim.x, tiles_n, tiles_m, tn, tm);
-    pipe_tile<WN, WM, TN, TM, UPS, NS, PACKED>(g, sg, tn, tm);
+    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, PACKED>(g, sg, tn, tm);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, bool PACKED>
-__global__ __launch_bounds__(64 * WN * WM) void gemm_pipe_grouped_kernel(GemmArgs g, SegTable tab,
-                                                                         uint32_t tiles_n) {
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED>
+__global__ __launch_bounds__(64 * WN * WM * KG) void gemm_pipe_grouped_kernel(GemmArgs g, SegTable tab,
+                                                                              uint32_t tiles_n) {
     const uint32_t tm = blockIdx.x / tiles_n;
     uint32_t i = 0;
     while (i + 1 < tab.nseg && tab.s[i + 1].tile0 <= tm)
         i++;
-    pipe_tile<WN, WM, TN, TM, UPS, NS, PACKED>(g, tab.s[i], blockIdx.x % tiles_n, tm - tab.s[i].tile0);
+    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, PACKED>(g, tab.s[i], blockIdx.x % tiles_n, tm - tab.s[i].tile0);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, bool PACKED>
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED>
 static void run_pipe1(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
     constexpr uint32_t BN = 16 * TN * WN, BM = 16 * TM * WM;
-    constexpr uint32_t threads = 64 * WN * WM;
+    constexpr uint32_t threads = 64 * WN * WM * KG;
     const uint32_t tiles_n = (g.rows + BN - 1) / BN;
     if (tab.nseg == 1) {
         const uint32_t tiles_m = (tab.s[0].T + BM - 1) / BM;
-        gemm_pipe_kernel<WN, WM, TN, TM, UPS, NS, PACKED><<<tiles_n * tiles_m, threads, 0, s>>>(g, tab.s[0], tiles_n, tiles_m);
+        gemm_pipe_kernel<WN, WM, TN, TM, UPS, NS, KG, PACKED><<<tiles_n * tiles_m, threads, 0, s>>>(g, tab.s[0], tiles_n, tiles_m);
     } else {
         SegTable t = tab;
         uint32_t tiles = 0;
@@ -1224,16 +1271,45 @@ static void run_pipe1(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
             t.s[i].tile0 = tiles;
             tiles += (t.s[i].T + BM - 1) / BM;
         }
-        gemm_pipe_grouped_kernel<WN, WM, TN, TM, UPS, NS, PACKED><<<tiles_n * tiles, threads, 0, s>>>(g, t, tiles_n);
+        gemm_pipe_grouped_kernel<WN, WM, TN, TM, UPS, NS, KG, PACKED><<<tiles_n * tiles, threads, 0, s>>>(g, t, tiles_n);
     }
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS>
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG>
+__global__ __launch_bounds__(64 * WN * WM * KG) void gemm_pipe_batch_kernel(JobTable tab) {
+    uint32_t j = 0;
+    while (j + 1 < tab.njobs && tab.wg0[j + 1] <= blockIdx.x)
+        j++;
+    const uint32_t b = blockIdx.x - tab.wg0[j];
+    if (b >= tab.tiles[j])
+        return;                                 /* padding up to the next job's multiple of 8 */
+    const uint32_t tiles_n = tab.tiles_n[j];
+    uint32_t tn, tm;
+    xcd_tile(b, tab.tiles[j], tiles_n, tab.tiles[j] / tiles_n, tn, tm);
+    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, true>(tab.g[j], tab.s[j], tn, tm);
+}
+
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG>
+static void run_pipe_batch(const JobTable &jobs, hipStream_t s) {
+    constexpr uint32_t BN = 16 * TN * WN, BM = 16 * TM * WM;
+    JobTable t = jobs;
+    uint32_t wg = 0;
+    for (uint32_t j = 0; j < t.njobs; j++) {
+        t.wg0[j] = wg;
+        t.tiles_n[j] = (t.g[j].rows + BN - 1) / BN;
+        t.tiles[j] = t.tiles_n[j] * ((t.s[j].T + BM - 1) / BM);
+        wg += (t.tiles[j] + 7) / 8 * 8;
+    }
+    t.wg0[t.njobs] = wg;
+    gemm_pipe_batch_kernel<WN, WM, TN, TM, UPS, NS, KG><<<wg, 64 * WN * WM * KG, 0, s>>>(t);
+}
+
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG = 1>
 static void run_pipe(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
     if (tab.s[0].qstride)
-        run_pipe1<WN, WM, TN, TM, UPS, NS, true>(g, tab, s);
+        run_pipe1<WN, WM, TN, TM, UPS, NS, KG, true>(g, tab, s);
     else
-        run_pipe1<WN, WM, TN, TM, UPS, NS, false>(g, tab, s);
+        run_pipe1<WN, WM, TN, TM, UPS, NS, KG, false>(g, tab, s);
 }
 
 /* The pipelined product's tile shapes: channels x frames, and the units of
@@ -1242,20 +1318,32 @@ struct RingCfg {
     const char *name;
     uint32_t bn, bm, ups;
     uint32_t slots;                 /* 0: ring_tile (four slots, four-stage passes) */
+    uint32_t kg;                    /* K groups of pipe_tile */
     void (*run)(const GemmArgs &, const SegTable &, hipStream_t);
+    void (*batch)(const JobTable &, hipStream_t);   /* pipe_tile only */
 };
 static const RingCfg kRing[] = {
     /* ring_tile: name <channels x frames, units a stage> */
-    { "ring<128x128,1>", 128, 128, 1, 0, run_ring<2, 2, 4, 4, 1> },
-    { "ring<64x64,1>", 64, 64, 1, 0, run_ring<2, 2, 2, 2, 1> },
-    { "ring<64x64,2>", 64, 64, 2, 0, run_ring<2, 2, 2, 2, 2> },
-    { "ring<64x64,4>", 64, 64, 4, 0, run_ring<2, 2, 2, 2, 4> },
+    { "ring<128x128,1>", 128, 128, 1, 0, 1, run_ring<2, 2, 4, 4, 1>, nullptr },
+    { "ring<64x64,1>", 64, 64, 1, 0, 1, run_ring<2, 2, 2, 2, 1>, nullptr },
+    { "ring<64x64,2>", 64, 64, 2, 0, 1, run_ring<2, 2, 2, 2, 2>, nullptr },
+    { "ring<64x64,4>", 64, 64, 4, 0, 1, run_ring<2, 2, 2, 2, 4>, nullptr },
     /* pipe_tile: name <channels x frames, units a stage, slots>; w8: eight
      * waves of 64 x 32 */
-    { "pipe<128x128,1,4>", 128, 128, 1, 4, run_pipe<2, 2, 4, 4, 1, 4> },
-    { "pipe<128x128w8,1,4>", 128, 128, 1, 4, run_pipe<2, 4, 4, 2, 1, 4> },
-    { "pipe<64x64,2,4>", 64, 64, 2, 4, run_pipe<2, 2, 2, 2, 2, 4> },
-    { "pipe<64x64,4,4>", 64, 64, 4, 4, run_pipe<2, 2, 2, 2, 4, 4> },
+    { "pipe<128x128,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 2, 4, 4, 1, 4, 1>, run_pipe_batch<2, 2, 4, 4, 1, 4, 1> },
+    { "pipe<128x128w8,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 4, 4, 2, 1, 4, 1>, run_pipe_batch<2, 4, 4, 2, 1, 4, 1> },
+    { "pipe<64x64,2,4>", 64, 64, 2, 4, 1, run_pipe<2, 2, 2, 2, 2, 4, 1>, run_pipe_batch<2, 2, 2, 2, 2, 4, 1> },
+    { "pipe<64x64,4,4>", 64, 64, 4, 4, 1, run_pipe<2, 2, 2, 2, 4, 4, 1>, run_pipe_batch<2, 2, 2, 2, 4, 4, 1> },
+    /* eight waves of 64 x 64 */
+    { "pipe<128x256w8,1,4>", 128, 256, 1, 4, 1, run_pipe<2, 4, 4, 4, 1, 4, 1>, run_pipe_batch<2, 4, 4, 4, 1, 4, 1> },
+    { "pipe<128x256w8,1,6>", 128, 256, 1, 6, 1, run_pipe<2, 4, 4, 4, 1, 6, 1>, run_pipe_batch<2, 4, 4, 4, 1, 6, 1> },
+    { "pipe<256x128w8,1,4>", 256, 128, 1, 4, 1, run_pipe<4, 2, 4, 4, 1, 4, 1>, run_pipe_batch<4, 2, 4, 4, 1, 4, 1> },
+    /* eight waves of 128 x 64 */
+    { "pipe<256x256w8,1,4>", 256, 256, 1, 4, 1, run_pipe<2, 4, 8, 4, 1, 4, 1>, run_pipe_batch<2, 4, 8, 4, 1, 4, 1> },
+    /* two K groups of four waves of 32 x 32 */
+    { "pipe<64x64,2,4,k2>", 64, 64, 2, 4, 2, run_pipe<2, 2, 2, 2, 2, 4, 2>, run_pipe_batch<2, 2, 2, 2, 2, 4, 2> },
+    { "pipe<64x64,1,4,k2>", 64, 64, 1, 4, 2, run_pipe<2, 2, 2, 2, 1, 4, 2>, run_pipe_batch<2, 2, 2, 2, 1, 4, 2> },
+    { "pipe<64x64,2,2,k2>", 64, 64, 2, 2, 2, run_pipe<2, 2, 2, 2, 2, 2, 2>, run_pipe_batch<2, 2, 2, 2, 2, 2, 2> },
 };
 constexpr int kNRing = sizeof kRing / sizeof kRing[0];
 
@@ -1278,7 +1366,7 @@ static bool fits(int i, uint32_t ku) {
     const RingCfg &c = kRing[i];
     if (c.slots == 0)
         return ku % (4 * c.ups) == 0;
-    return ku % c.ups == 0 && ku / c.ups >= c.slots;
+    return ku % (c.kg * c.ups) == 0 && ku / (c.kg * c.ups) >= c.slots;
 }
 
 static int pick_ring(uint32_t rows, uint64_t frames, uint32_t ku) {
@@ -1287,11 +1375,14 @@ static int pick_ring(uint32_t rows, uint64_t frames, uint32_t ku) {
     auto tiles = [&](int i) { return (uint64_t)((rows + kRing[i].bn - 1) / kRing[i].bn) * ((frames + kRing[i].bm - 1) / kRing[i].bm); };
     /* measured on the layer's shapes at 750 and 7500 frames (every tiling,
      * every product): a CU's worth of 128 x 128 tiles takes the eight-wave
-     * pipelined tile; fewer take 64 x 64 pipelined tiles of two-unit stages;
+     * pipelined tile; fewer take 64 x 64 pipelined tiles of two-unit stages,
+     * split into two K groups where the inputs are deep;
      * inputs too short for their slots take the ring, 64 x 64, with longer
      * stages the fewer the tiles */
     if (tiles(0) >= 256 && fits(5, ku))
         return 5;
+    if (ku >= 32 && tiles(6) < 512 && fits(13, ku))
+        return 13;          /* deep inputs, few tiles: two K groups a tile */
     if (fits(6, ku))
         return 6;
     const uint64_t t64 = tiles(1);
@@ -1377,6 +1468,35 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
     }
     *name = buf;
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_gemm_batch(const JobTable &jobs, hipStream_t s, const char **name) {
+    uint32_t rows = 0;
+    uint64_t frames = 0;
+    for (uint32_t j = 0; j < jobs.njobs; j++) {
+        rows = jobs.g[j].rows > rows ? jobs.g[j].rows : rows;
+        frames += jobs.s[j].T;
+    }
+    if (jobs.njobs == 0 || frames == 0)
+        return 0;
+    /* the tiling the jobs would take as one product of their frames */
+    const int c = pick_ring(rows, frames, jobs.g[0].ku);
+    if (kRing[c].batch) {
+        kRing[c].batch(jobs, s);
+        *name = kRing[c].name;
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    /* inputs too short for the pipelined tile: one launch a job */
+    for (uint32_t j = 0; j < jobs.njobs; j++) {
+        if (jobs.s[j].T == 0)
+            continue;
+        SegTable t;
+        t.nseg = 1;
+        t.s[0] = jobs.s[j];
+        if (launch_gemm(jobs.g[j], t, s, name))
+            return -1;
+    }
+    return 0;
 }
 
 }  // namespace pkq8

@@ -205,3 +205,58 @@ def test_packed_path(hip, torch, M, K, N):
                 assert np.array_equal(bits(out.cpu().numpy()), bits(r)), (ti, hip.last_kernel())
         finally:
             hip.force_tiling(-1)
+
+
+@pytest.mark.parametrize("K", [1024, 4096, 128])
+def test_batch_of_products(hip, torch, K):
+    """Independent products in one launch (the attention's q, k, v and the
+    positions' projection at once): each job's outputs are the bits its own
+    launch gives, with jobs of different frame counts, channel counts, a run
+    of interior panels, bias and add; under the heuristic and under every
+    tiling (short inputs fall back to one launch a job)."""
+    dev = torch.device("cuda")
+    g = synth.rng(K + 17)
+    specs = [(37, 1024, 0, 1024, False, 0), (750, 1024, 0, 1024, True, 1), (1, 512, 0, 512, False, 0),
+             (1499, 1040, 16, 1008, True, 0), (0, 256, 0, 256, False, 0), (200, 2048, 32, 96, False, 1)]
+    mats, jobs, singles = [], [], []
+    for (T, N, r0, rows, use_bias, add) in specs:
+        w = synth.pack_q8(synth.weights(g, N, K))
+        ws = synth.scales(g, N)
+        m = hip.Q8Matrix(w, ws)
+        mats.append(m)
+        x = torch.from_numpy(synth.activations(g, max(T, 1), K)).to(dev)
+        qp = torch.zeros((hip.packed_bytes(K, max(T, 1)),), dtype=torch.int8, device=dev)
+        d = torch.empty((max(T, 1),), dtype=torch.float32, device=dev)
+        if T:
+            hip.quantize_packed_dev(None, qp, d, x, K, T, K)
+        bias = torch.from_numpy(g.standard_normal(N).astype(np.float32)).to(dev) if use_bias else None
+        os_ = N + 3
+        base = torch.from_numpy(g.standard_normal(max(T, 1) * os_).astype(np.float32)).to(dev)
+        ws_ptr = m.dev_scales + 4 * r0
+        bias_v = bias[r0:] if bias is not None else None
+        singles.append((base, os_, m, r0, rows, ws_ptr, bias_v, qp, d, T, add))
+    torch.cuda.synchronize()
+    want = []
+    for (base, os_, m, r0, rows, ws_ptr, bias_v, qp, d, T, add) in singles:
+        out = base.clone()
+        if T:
+            hip.gemm_q8_packed_dev(None, os_, m, r0, rows, ws_ptr, bias_v, qp, d, K, T, add,
+                                   out_ptr=out.data_ptr() + 4 * r0)
+        want.append(out)
+    torch.cuda.synchronize()
+    try:
+        for ti in [-1] + list(range(hip.tilings())):
+            hip.force_tiling(ti)
+            outs = [b.clone() for (b, *_rest) in singles]
+            jobs = []
+            for o, (base, os_, m, r0, rows, ws_ptr, bias_v, qp, d, T, add) in zip(outs, singles):
+                jobs.append((o[r0:], os_, m, r0, rows, ws_ptr, bias_v, qp, d, K, T, add))
+            say("batch", K, ti)
+            hip.gemm_q8_batch_dev(jobs)
+            torch.cuda.synchronize()
+            for j, (o, wnt) in enumerate(zip(outs, want)):
+                assert np.array_equal(bits(o.cpu().numpy()), bits(wnt.cpu().numpy())), (ti, j, hip.last_kernel())
+    finally:
+        hip.force_tiling(-1)
+        for m in mats:
+            m.release()
