@@ -492,6 +492,32 @@ def main():
     cpu = None
     host_inputs = [(p.x_host.reshape(-1), p.w, p.ws, p.M, p.K, p.N, p.add) for p in prods]
     log(f"layer: {ms:.4f} ms a step, {tops:.1f} TOPS; dominant {dom.name} {dkms * 1e3:.2f} us")
+    # the real encoder's blocks (qb = 32 by default, 64 in its fast mode): the
+    # same layer with blocked quantizes and products on the packed path (one
+    # launch a product: the batch takes per-row blocks only)
+    blocked = {}
+    for qb in (32, 64):
+        bd = {p.name: torch.empty((p.M * p.K // qb,), dtype=torch.float32, device=p.x.device) for p in prods}
+        src = {p.name: p for p in prods}
+        owner = {"k": "q", "v": "q"}
+        pos = src["pos"]
+        pk.quantize_packed_dev(None, pos.qp, bd["pos"], pos.x, pos.K, pos.M, pos.xs, qb=qb)  # once an encode
+
+        def blocked_step(qb=qb, bd=bd):
+            for p in prods:
+                o = src[owner.get(p.name, p.name)]
+                if p.name not in owner and p.name != "pos":
+                    pk.quantize_packed_dev(None, p.qp, bd[p.name], p.x, p.K, p.M, p.xs, qb=qb)
+                pk.gemm_q8_packed_dev(p.out, p.N, p.m, 0, p.N, p.m.dev_scales, None, o.qp, bd[o.name], p.K, p.M,
+                                      p.add, qb=qb)
+        gb = graph_of(torch, blocked_step)
+        bms = time_graph(torch, gb, 50, 5)
+        blocked[f"qb{qb}"] = dict(ms_per_step=round(bms, 4), tops=round(ops / (bms * 1e-3) / 1e12, 1),
+                                  kernel=pk.last_kernel())
+        log(f"layer qb={qb}: {bms:.4f} ms")
+        del gb
+    extra["layer_M750_blocked"] = blocked
+
     if not args.quick:
         # the long-form layer, M = 7500 (one segment of ten minutes)
         long_prods = make_layer(pk, torch, 7500, seed=2)

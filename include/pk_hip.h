@@ -138,13 +138,14 @@ int pk_hip_gemm_q8_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, u
 /* Bytes a packed copy of T columns of n inputs takes. */
 size_t pk_hip_packed_bytes(uint32_t n, uint32_t T);
 
-/* quantize (per-row blocks only: a->qb == a->n, n <= 4096) writing d and
- * the packed copy qp, and the row-major a->q too unless it is NULL. Device
- * pointers; qp 16-byte aligned and pk_hip_packed_bytes(n, T) long. */
+/* quantize (blocks of the whole row, or of 32 or 64 inputs: the encoder's
+ * modes; n <= 4096) writing d and the packed copy qp, and the row-major a->q
+ * too unless it is NULL. Device pointers; qp 16-byte aligned and
+ * pk_hip_packed_bytes(n, T) long. */
 int pk_hip_quantize_packed_dev(pk_hip_act *a, int8_t *qp, const float *x, size_t xs, void *stream);
 
 /* gemm_q8_dev with the activations read from the packed copy qp (a->q is
- * not read; a->d, n, qb == n and T are). */
+ * not read; a->d, n, qb and T are; qb the whole row, 32 or 64). */
 int pk_hip_gemm_q8_packed_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
                               const float *ws, const float *bias, const pk_hip_act *a, const int8_t *qp,
                               int add, int rmode, void *stream);

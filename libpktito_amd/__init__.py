@@ -243,16 +243,19 @@ def packed_bytes(n, T):
     return lib().pk_hip_packed_bytes(n, T)
 
 
-def quantize_packed_dev(q, qp, d, x, n, T, xs, stream=None):
-    """Per-row quantize on device tensors into the packed copy qp (uint8/int8,
-    packed_bytes(n, T) long), and into q [T, n] unless q is None."""
-    a = Act(_dptr(q), _dptr(d), n, n, T)
+def quantize_packed_dev(q, qp, d, x, n, T, xs, stream=None, qb=None):
+    """Quantize on device tensors into the packed copy qp (uint8/int8,
+    packed_bytes(n, T) long), and into q [T, n] unless q is None; blocks of
+    qb inputs (the whole row by default; 32 or 64)."""
+    a = Act(_dptr(q), _dptr(d), n, qb or n, T)
     _check(lib().pk_hip_quantize_packed_dev(ctypes.byref(a), _dptr(qp), _dptr(x), xs, _stream(stream)))
 
 
-def gemm_q8_packed_dev(out, os_, m, r0, rows, ws_ptr, bias, qp, d, n, T, add, rmode=0, stream=None, out_ptr=None):
-    """gemm_q8 on device tensors with the activations from the packed copy qp."""
-    a = Act(None, _dptr(d), n, n, T)
+def gemm_q8_packed_dev(out, os_, m, r0, rows, ws_ptr, bias, qp, d, n, T, add, rmode=0, stream=None, out_ptr=None,
+                       qb=None):
+    """gemm_q8 on device tensors with the activations from the packed copy qp
+    (blocks of qb inputs: the whole row by default, or 32 or 64)."""
+    a = Act(None, _dptr(d), n, qb or n, T)
     op = out_ptr if out_ptr is not None else _dptr(out)
     _check(lib().pk_hip_gemm_q8_packed_dev(op, os_, m.handle, r0, rows, ws_ptr, _dptr(bias), ctypes.byref(a),
                                            _dptr(qp), int(add), rmode, _stream(stream)))

@@ -610,13 +610,14 @@ int pk_hip_quantize_packed_dev(pk_hip_act *a, int8_t *qp, const float *x, size_t
         return fail(PK_HIP_EINVAL, "quantize_packed_dev: act is NULL");
     if (a->T == 0)
         return PK_HIP_OK;
-    if (!a->d || !qp || a->qb != a->n || a->n == 0 || a->n % 32 || a->n > 4096)
-        return fail(PK_HIP_EINVAL, "quantize_packed_dev: per-row blocks (qb == n), n a multiple of 32 "
-                                   "up to 4096, d and qp set");
+    if (!a->d || !qp || a->n == 0 || a->n % 32 || a->n > 4096 ||
+        !(a->qb == a->n || ((a->qb == 32 || a->qb == 64) && a->n % a->qb == 0)))
+        return fail(PK_HIP_EINVAL, "quantize_packed_dev: blocks of the whole row, 32 or 64 inputs, n a "
+                                   "multiple of 32 up to 4096, d and qp set");
     if (xs < a->n || xs % 4 || ((uintptr_t)x & 15) || ((uintptr_t)qp & 15) || ((uintptr_t)a->q & 15))
         return fail(PK_HIP_EINVAL, "quantize_packed_dev: x, q and qp 16-byte aligned, xs >= n and a multiple of 4");
     const char *name = "";
-    if (pkq8::launch_quantize_packed(a->q, qp, a->d, x, xs, a->n, a->T, (hipStream_t)stream, &name))
+    if (pkq8::launch_quantize_packed(a->q, qp, a->d, x, xs, a->n, a->qb, a->T, (hipStream_t)stream, &name))
         return hip_fail(hipGetLastError(), "quantize_packed launch");
     g_kernel = name;
     return PK_HIP_OK;
@@ -634,8 +635,10 @@ int pk_hip_gemm_q8_packed_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_
         return fail(PK_HIP_EINVAL, "gemm_q8_packed_dev: act is NULL");
     if (a->T == 0)
         return PK_HIP_OK;
-    if (!a->d || !qp || ((uintptr_t)qp & 15) || a->qb != a->n || a->n % 32 || a->n > 16384)
-        return fail(PK_HIP_EINVAL, "gemm_q8_packed_dev: per-row blocks (qb == n), d and a 16-byte aligned qp");
+    if (!a->d || !qp || ((uintptr_t)qp & 15) || a->n % 32 || a->n > 16384 ||
+        !(a->qb == a->n || ((a->qb == 32 || a->qb == 64) && a->n % a->qb == 0)))
+        return fail(PK_HIP_EINVAL, "gemm_q8_packed_dev: blocks of the whole row, 32 or 64 inputs, d and a "
+                                   "16-byte aligned qp");
     if (!out || !ws)
         return fail(PK_HIP_EINVAL, "gemm_q8_packed_dev: out or ws is NULL");
     if (a->T > 1 && os < rows)

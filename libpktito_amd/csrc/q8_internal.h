@@ -74,10 +74,10 @@ int launch_repack(int8_t *dst, const int8_t *src, uint32_t rows, uint32_t cols, 
 int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb,
                     uint32_t T, hipStream_t s, const char **name);
 
-/* Per-row quantize (qb == n, n <= 4096) writing the packed copy qp, and the
- * row-major q too when q is not NULL. */
+/* Quantize (n <= 4096; qb == n, 32 or 64) writing the packed copy qp, and
+ * the row-major q too when q is not NULL. */
 int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
-                           uint32_t T, hipStream_t s, const char **name);
+                           uint32_t qb, uint32_t T, hipStream_t s, const char **name);
 
 /* The pipelined product's tilings: how many, and forcing one (-1: the
  * heuristic); returns the one forced before. */

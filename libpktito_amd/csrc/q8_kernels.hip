@@ -212,7 +212,23 @@ __global__ __launch_bounds__(256) void quant_any_kernel(int8_t *__restrict__ q, 
 /* A whole column is one block, n <= 4096: one wave a column, four columns a
  * workgroup, each lane CH float4 chunks of it (chunk c of lane l is float4
  * l + 64 c), every load issued before the first is used. */
-template <int CH, bool PACK>
+/* max of a non-negative int over aligned groups of W lanes (W = 8 or 16), in
+ * every lane of the group: DPP quad swaps, half mirror, and mirror for 16 */
+template <int W>
+__device__ __forceinline__ int group_max_nonneg(int v) {
+    static_assert(W == 8 || W == 16, "groups of 8 or 16 lanes");
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
+    if constexpr (W == 16)
+        v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
+    return v;
+}
+
+/* One wave a column of n <= 4096 inputs, four columns a workgroup. QB == 0:
+ * the column is one block; QB == 32 or 64: blocks of QB inputs, each the
+ * QB / 4 lanes holding it, reduced within those lanes. */
+template <int CH, bool PACK, int QB>
 __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q, int8_t *__restrict__ qp,
                                                          float *__restrict__ d, const float *__restrict__ x,
                                                          size_t xs, uint32_t n, uint32_t T) {
@@ -228,17 +244,39 @@ __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q,
         const uint32_t i = lane + 64 * c;
         v[c] = i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    int m = 0;
+    auto mag4 = [](float4 f) {
+        return max(max(mag_bits(f.x), mag_bits(f.y)), max(mag_bits(f.z), mag_bits(f.w)));
+    };
+    /* the scale of each chunk's block: one for the column, or one a chunk */
+    float dv[QB ? CH : 1], id[QB ? CH : 1];
+    bool zero[QB ? CH : 1];
+    if constexpr (QB == 0) {
+        int m = 0;
 #pragma unroll
-    for (int c = 0; c < CH; c++)
-        m = max(max(max(m, mag_bits(v[c].x)), max(mag_bits(v[c].y), mag_bits(v[c].z))), mag_bits(v[c].w));
-    const uint32_t mb = (uint32_t)wave_max_nonneg(m);
-    const bool zero = zero_bits(mb);
-    float dv = 0.0f, id = 0.0f;
-    if (!zero) {
-        const float amax = __uint_as_float(mb);
-        dv = amax / 127.0f;
-        id = 127.0f / amax;
+        for (int c = 0; c < CH; c++)
+            m = max(m, mag4(v[c]));
+        const uint32_t mb = (uint32_t)wave_max_nonneg(m);
+        zero[0] = zero_bits(mb);
+        dv[0] = 0.0f;
+        id[0] = 0.0f;
+        if (!zero[0]) {
+            const float amax = __uint_as_float(mb);
+            dv[0] = amax / 127.0f;
+            id[0] = 127.0f / amax;
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const uint32_t mb = (uint32_t)group_max_nonneg<QB / 4>(mag4(v[c]));
+            zero[c] = zero_bits(mb);
+            dv[c] = 0.0f;
+            id[c] = 0.0f;
+            if (!zero[c]) {
+                const float amax = __uint_as_float(mb);
+                dv[c] = amax / 127.0f;
+                id[c] = 127.0f / amax;
+            }
+        }
     }
     int *qr = (int *)(q + (size_t)t * n);
     /* packed: row t is row t % 16 of group t / 16; inputs k..k+3 of unit
@@ -247,34 +285,44 @@ __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q,
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
+        const int cb = QB ? c : 0;
         if (i < n4) {
-            const int v4 = zero ? 0 : pack4(v[c], id);
+            const int v4 = zero[cb] ? 0 : pack4(v[c], id[cb]);
             if (!PACK || q)
                 qr[i] = v4;
             if (PACK) {
                 const uint32_t k = 4 * i, u = k >> 6, kq = (k >> 4) & 3;
                 *(int *)(qp + ((size_t)u * G + g) * kUnitBytes + (kq * 16 + r) * 16 + (k & 15)) = v4;
             }
+            if (QB && (i & (QB / 4 - 1)) == 0)
+                d[(size_t)t * (n / QB) + (4 * i) / QB] = dv[cb];
         }
     }
-    if (lane == 0)
-        d[t] = dv;
+    if (QB == 0 && lane == 0)
+        d[t] = dv[0];
 }
 
 int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
-                           uint32_t T, hipStream_t s, const char **name) {
+                           uint32_t qb, uint32_t T, hipStream_t s, const char **name) {
     if (T == 0)
         return 0;
     const uint32_t n4 = n / 4, grid4 = (T + 3) / 4;
-    if (n4 <= 256) {
-        quant_wave_kernel<4, true><<<grid4, 256, 0, s>>>(q, qp, d, x, xs, n, T);
-        *name = "quant_wave_packed<4>";
-    } else if (n4 <= 1024) {
-        quant_wave_kernel<16, true><<<grid4, 256, 0, s>>>(q, qp, d, x, xs, n, T);
-        *name = "quant_wave_packed<16>";
-    } else {
+    if (n4 > 1024 || !(qb == n || qb == 32 || qb == 64))
         return -2;
+    const bool small = n4 <= 256;
+#define PK_QW(CH, QB, NAME)                                                          \
+    do {                                                                             \
+        quant_wave_kernel<CH, true, QB><<<grid4, 256, 0, s>>>(q, qp, d, x, xs, n, T); \
+        *name = NAME;                                                                \
+    } while (0)
+    if (qb == n) {
+        if (small) PK_QW(4, 0, "quant_wave_packed<4>"); else PK_QW(16, 0, "quant_wave_packed<16>");
+    } else if (qb == 32) {
+        if (small) PK_QW(4, 32, "quant_wave_packed<4,qb32>"); else PK_QW(16, 32, "quant_wave_packed<16,qb32>");
+    } else {
+        if (small) PK_QW(4, 64, "quant_wave_packed<4,qb64>"); else PK_QW(16, 64, "quant_wave_packed<16,qb64>");
     }
+#undef PK_QW
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -284,11 +332,21 @@ int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, 
         return 0;
     const uint32_t nch = n / 16, n4 = n / 4, grid4 = (T + 3) / 4;
     if (qb == n && n4 <= 256) {
-        quant_wave_kernel<4, false><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
+        quant_wave_kernel<4, false, 0><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
         *name = "quant_wave<4>";
     } else if (qb == n && n4 <= 1024) {
-        quant_wave_kernel<16, false><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
+        quant_wave_kernel<16, false, 0><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
         *name = "quant_wave<16>";
+    } else if ((qb == 32 || qb == 64) && n4 <= 1024) {
+        if (qb == 32) {
+            if (n4 <= 256) quant_wave_kernel<4, false, 32><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
+            else quant_wave_kernel<16, false, 32><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
+            *name = "quant_wave<qb32>";
+        } else {
+            if (n4 <= 256) quant_wave_kernel<4, false, 64><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
+            else quant_wave_kernel<16, false, 64><<<grid4, 256, 0, s>>>(q, nullptr, d, x, xs, n, T);
+            *name = "quant_wave<qb64>";
+        }
     } else if (qb == n && nch <= 1024) {
         quant_col_kernel<4, 4><<<T, 256, 0, s>>>(q, d, x, xs, n);
         *name = "quant_col<4,4>";
@@ -918,7 +976,23 @@ __device__ __forceinline__ void ring_tile(const GemmArgs &g, const Seg &sg, uint
  * that barrier and takes stage s + NS at once; NS - 1 stages are in flight
  * while one is multiplied. */
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED>
+/* 4 bytes from LDS, issued as written; the caller waits on lgkmcnt */
+__device__ __forceinline__ float lds_read4(uint32_t addr) {
+    float r;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+    return r;
+}
+
+/* BLK: 0, a block a column (qb == n); 1, blocks of one unit (qb == 64);
+ * 2, blocks of half a unit (qb == 32). With blocks, each block's exact int32
+ * sum comes from MFMAs of its own (a unit's two halves by masking the weight
+ * fragment to the lanes holding that half's inputs, lanes 0-31 holding
+ * inputs 0-31 of the unit and lanes 32-63 the rest), and enters ref's chain
+ * acc = fmaf((float)s, d, acc) in block order; blocks past n (padding units)
+ * are skipped. The stage's block scales ride with its units: each slot ends
+ * with BM frames x the stage's blocks of d, frame-contiguous, loaded by DMA
+ * with the units and read a sub-step ahead with the fragments. */
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED, int BLK>
 __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint32_t tn, uint32_t tm) {
     constexpr int NW = WN * WM;             /* waves of one K group */
     constexpr int BN = 16 * TN * WN, BM = 16 * TM * WM;
@@ -926,9 +1000,14 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
     constexpr int SLOTU = UNITS * UPS;
     static_assert(SLOTU % NW == 0, "each wave loads whole units");
     constexpr int L = SLOTU / NW;
+    constexpr int BPU = BLK == 2 ? 2 : 1, BPS = BLK ? BPU * UPS : 0;     /* blocks a unit, a stage */
+    static_assert(BLK == 0 || (KG == 1 && BM % 64 == 0), "blocks: one K group, whole 64-frame chunks");
+    constexpr int DCH = BLK ? BM * BPS / 64 : 0;                          /* 64-float chunks of d a stage */
+    constexpr int LD = (DCH + NW - 1) / NW, LT = L + LD;                  /* loads a wave issues a stage */
     static_assert(NS >= 2 && NS <= 8, "two to eight slots");
-    static_assert((NS - 1) * L < 64, "the stages in flight fit vmcnt");
-    constexpr int SLOT = SLOTU * kUnitBytes;
+    static_assert((NS - 1) * LT < 64, "the stages in flight fit vmcnt");
+    constexpr int DB = BLK ? (BM * BPS * 4 + kUnitBytes - 1) / kUnitBytes * kUnitBytes : 0;
+    constexpr int SLOT = SLOTU * kUnitBytes + DB;
     static_assert(KG * NS * SLOT <= 160 * 1024, "the slots fit a CU's LDS");
     static_assert(KG == 1 || (KG - 1) * NW * TN * TM * kUnitBytes <= NS * SLOT, "the partial sums fit a ring");
     static_assert((UPS & (UPS - 1)) == 0, "a power of two units a stage");
@@ -946,7 +1025,7 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
     const uint32_t T = sg.T;
     const uint32_t n0 = tn * BN, m0 = tm * BM;
     const uint32_t npan = g.rows >> 4;
-    const uint32_t n = g.n, kug = g.ku / KG, u0 = kg * kug, ns = kug / UPS;
+    const uint32_t n = g.n, kug = g.ku / KG, u0 = kg * kug, ns = kug / UPS, nb = g.nb;
 
     if (g.rmode)
         __builtin_amdgcn_s_setreg(2049, g.rmode);    /* MODE.FP_ROUND, single precision */
@@ -992,6 +1071,21 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
             }
             __builtin_amdgcn_global_load_lds(PK_AS1(gp), PK_AS3(slot + (wave * L + s) * kUnitBytes), 16, 0, 0);
         }
+        if constexpr (BLK != 0) {
+            /* chunk c: block c / (BM / 64) of the stage, frames (c % (BM / 64)) * 64 + lane;
+             * a wave past the last chunk loads the last one again (the same bytes) */
+#pragma unroll
+            for (int i = 0; i < LD; i++) {
+                const int c = wave + NW * i < DCH ? wave + NW * i : DCH - 1;
+                const int blk = c / (BM / 64), fc = c % (BM / 64);
+                uint32_t f = m0 + fc * 64 + lane;
+                f = f < T ? f : T - 1;
+                uint32_t bi = (u0 + j * UPS) * BPU + blk;
+                bi = bi < nb ? bi : nb - 1;
+                __builtin_amdgcn_global_load_lds(PK_AS1(sg.d + (size_t)f * nb + bi),
+                                                 PK_AS3(slot + SLOTU * kUnitBytes + (blk * BM + fc * 64) * 4), 4, 0, 0);
+            }
+        }
     };
 
     v4i acc[TN][TM];
@@ -1000,21 +1094,42 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
 #pragma unroll
         for (int j = 0; j < TM; j++)
             acc[i][j] = v4i{0, 0, 0, 0};
+    float4 accf[BLK ? TN : 1][BLK ? TM : 1];
+#pragma unroll
+    for (int i = 0; i < (BLK ? TN : 1); i++)
+#pragma unroll
+        for (int j = 0; j < (BLK ? TM : 1); j++)
+            accf[i][j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
     const uint32_t wbase = lds_addr(ring) + (wn * TN) * kUnitBytes + lane * 16;
     const uint32_t abase = lds_addr(ring) + (UB + wm * TM) * kUnitBytes + lane * 16;
+    /* this lane's frame within the tile for frame tile j: (wm TM + j) 16 + lane % 16 */
+    const uint32_t dbase = lds_addr(ring) + SLOTU * kUnitBytes + ((wm * TM) * 16 + (lane & 15)) * 4;
     /* LDS offset of sub-step gi's fragments */
     auto at_of = [&](uint32_t gi) {
         const uint32_t s = gi / UPS, kk = gi % UPS;
         return (s % NS) * SLOT + kk * UNITS * kUnitBytes;
     };
-    auto read_set = [&](v4i (&f)[R], uint32_t at) {
+    struct Set {
+        v4i f[R];
+        float dv[BLK ? TM * BPU : 1];
+    };
+    auto read_set = [&](Set &st, uint32_t gi) {
+        const uint32_t at = at_of(gi);
 #pragma unroll
         for (int i = 0; i < TN; i++)
-            f[i] = lds_read16(wbase + at + i * kUnitBytes);
+            st.f[i] = lds_read16(wbase + at + i * kUnitBytes);
 #pragma unroll
         for (int j = 0; j < TM; j++)
-            f[TN + j] = lds_read16(abase + at + j * kUnitBytes);
+            st.f[TN + j] = lds_read16(abase + at + j * kUnitBytes);
+        if constexpr (BLK != 0) {
+            const uint32_t s = gi / UPS, kk = gi % UPS;
+#pragma unroll
+            for (int h = 0; h < BPU; h++)
+#pragma unroll
+                for (int j = 0; j < TM; j++)
+                    st.dv[h * TM + j] = lds_read4(dbase + (s % NS) * SLOT + ((kk * BPU + h) * BM + j * 16) * 4);
+        }
     };
     /* Sub-step gi multiplies the fragments read a sub-step ago (cur) and
      * reads gi + 1's (nxt). At the last sub-step of stage s < ns - 1 the
@@ -1022,32 +1137,72 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
      * loads may stay in flight) and meets, and with ISSUE refills stage s's
      * slot with stage s + NS. Every choice is a template argument, so the
      * loop below has no branch but its own and the accumulators stay put. */
-    auto step = [&](uint32_t gi, auto barrier, auto later, auto refill, auto more, v4i (&cur)[R],
-                    v4i (&nxt)[R]) {
+    auto step = [&](uint32_t gi, auto barrier, auto later, auto refill, auto more, Set &cur, Set &nxt) {
         wait_lgkm<0>();
 #pragma unroll
         for (int r = 0; r < R; r++)
-            asm volatile("" : "+v"(cur[r]));
+            asm volatile("" : "+v"(cur.f[r]));
+        if constexpr (BLK != 0) {
+#pragma unroll
+            for (int r = 0; r < TM * BPU; r++)
+                asm volatile("" : "+v"(cur.dv[r]));
+        }
         if constexpr (decltype(barrier)::value) {
-            wait_vm<decltype(later)::value * L>();
+            wait_vm<decltype(later)::value * LT>();
             __builtin_amdgcn_s_barrier();
             if constexpr (decltype(refill)::value)
                 issue(gi / UPS + NS);
         }
         if constexpr (decltype(more)::value)
-            read_set(nxt, at_of(gi + 1));
+            read_set(nxt, gi + 1);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (BLK == 0) {
 #pragma unroll
-        for (int i = 0; i < TN; i++)
+            for (int i = 0; i < TN; i++)
 #pragma unroll
-            for (int j = 0; j < TM; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur[i], cur[TN + j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < TM; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.f[i], cur.f[TN + j], acc[i][j], 0, 0, 0);
+        } else {
+            const uint32_t u = u0 + gi;             /* the unit: uniform */
+#pragma unroll
+            for (int h = 0; h < BPU; h++) {
+                v4i fw[TN];
+#pragma unroll
+                for (int i = 0; i < TN; i++) {
+                    if constexpr (BLK == 2) {
+                        const bool mine = (lane >> 5) == h;
+                        fw[i] = v4i{mine ? cur.f[i][0] : 0, mine ? cur.f[i][1] : 0, mine ? cur.f[i][2] : 0,
+                                    mine ? cur.f[i][3] : 0};
+                    } else {
+                        fw[i] = cur.f[i];
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < TN; i++)
+#pragma unroll
+                    for (int j = 0; j < TM; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], cur.f[TN + j], v4i{0, 0, 0, 0}, 0,
+                                                                          0, 0);
+                if (u * BPU + h < nb) {
+#pragma unroll
+                    for (int i = 0; i < TN; i++)
+#pragma unroll
+                        for (int j = 0; j < TM; j++) {
+                            const float dvj = cur.dv[h * TM + j];
+                            accf[i][j].x = __builtin_fmaf((float)acc[i][j][0], dvj, accf[i][j].x);
+                            accf[i][j].y = __builtin_fmaf((float)acc[i][j][1], dvj, accf[i][j].y);
+                            accf[i][j].z = __builtin_fmaf((float)acc[i][j][2], dvj, accf[i][j].z);
+                            accf[i][j].w = __builtin_fmaf((float)acc[i][j][3], dvj, accf[i][j].w);
+                        }
+                }
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
     };
     using yes = std::true_type;
     using no = std::false_type;
-    v4i f0[R], f1[R];
-    auto setpair = [&](auto k) -> auto & {
+    Set f0, f1;
+    auto setpair = [&](auto k) -> Set & {
         if constexpr (decltype(k)::value % 2 == 0) return f0; else return f1;
     };
 
@@ -1056,12 +1211,13 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
      * the wait for stage 0 covers them, and the epilogue finds them in LDS
      * instead of waiting a memory round trip after the last MFMA. Each
      * segment is whole 64-float chunks; indexes past the tile's frames or
-     * channels read the last one (their results are never stored). */
+     * channels read the last one (their results are never stored). With
+     * blocks the frame scales are not used (the chain took them). */
     constexpr int ED = (BM + 63) / 64, EW = (BN + 63) / 64, ECH = ED + 2 * EW;
     __shared__ __attribute__((aligned(256))) float epi[ECH * 64];
     if (kg == 0) {
         const int nch = g.bias ? ECH : ED + EW;
-        for (int c = wave; c < nch; c += NW) {
+        for (int c = BLK ? ED + wave : wave; c < nch; c += NW) {
             const float *a;
             if (c < ED) {
                 const uint32_t t = m0 + c * 64 + lane;
@@ -1078,7 +1234,7 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
 #pragma unroll
     for (int j = 0; j < NS; j++)
         issue(j);
-    wait_vm<(NS - 1) * L>();
+    wait_vm<(NS - 1) * LT>();
     __builtin_amdgcn_s_barrier();
     read_set(f0, 0);
 
@@ -1138,7 +1294,7 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
         const uint32_t t = m0 + (wm * TM + j) * 16 + (lane & 15);
         if (t >= T)
             continue;
-        const float dt = epi[t - m0];
+        const float dt = BLK ? 0.0f : epi[t - m0];
 #pragma unroll
         for (int i = 0; i < TN; i++) {
             const uint32_t c = n0 + (wn * TN + i) * 16 + (lane >> 4) * 4;
@@ -1152,12 +1308,21 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
                 bsr[0] = bv.x; bsr[1] = bv.y; bsr[2] = bv.z; bsr[3] = bv.w;
             }
             float v[4];
+            if constexpr (BLK != 0) {
+                const float4 af = accf[i][j];
+                const float a4[4] = { af.x, af.y, af.z, af.w };
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                v[r] = __builtin_fmaf((float)acc[i][j][r], dt, 0.0f) * wsr[r];
+                for (int r = 0; r < 4; r++)
+                    v[r] = a4[r] * wsr[r];
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    v[r] = __builtin_fmaf((float)acc[i][j][r], dt, 0.0f) * wsr[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++)
                 if (g.bias)
                     v[r] = v[r] + bsr[r];
-            }
             float *o = sg.out + (size_t)t * sg.os + c;
             if (vec) {
                 float4 ov = make_float4(v[0], v[1], v[2], v[3]);
@@ -1238,32 +1403,32 @@ static void run_ring(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
         run_ring1<WN, WM, TN, TM, UPS, false>(g, tab, s);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED>
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED, int BLK>
 __global__ __launch_bounds__(64 * WN * WM * KG) void gemm_pipe_kernel(GemmArgs g, Seg sg, uint32_t tiles_n,
                                                                       uint32_t tiles_m) {
     uint32_t tn, tm;
     xcd_tile(blockIdx.x, gridDim.x, tiles_n, tiles_m, tn, tm);
-    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, PACKED>(g, sg, tn, tm);
+    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, PACKED, BLK>(g, sg, tn, tm);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED>
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED, int BLK>
 __global__ __launch_bounds__(64 * WN * WM * KG) void gemm_pipe_grouped_kernel(GemmArgs g, SegTable tab,
                                                                               uint32_t tiles_n) {
     const uint32_t tm = blockIdx.x / tiles_n;
     uint32_t i = 0;
     while (i + 1 < tab.nseg && tab.s[i + 1].tile0 <= tm)
         i++;
-    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, PACKED>(g, tab.s[i], blockIdx.x % tiles_n, tm - tab.s[i].tile0);
+    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, PACKED, BLK>(g, tab.s[i], blockIdx.x % tiles_n, tm - tab.s[i].tile0);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED>
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, bool PACKED, int BLK>
 static void run_pipe1(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
     constexpr uint32_t BN = 16 * TN * WN, BM = 16 * TM * WM;
     constexpr uint32_t threads = 64 * WN * WM * KG;
     const uint32_t tiles_n = (g.rows + BN - 1) / BN;
     if (tab.nseg == 1) {
         const uint32_t tiles_m = (tab.s[0].T + BM - 1) / BM;
-        gemm_pipe_kernel<WN, WM, TN, TM, UPS, NS, KG, PACKED><<<tiles_n * tiles_m, threads, 0, s>>>(g, tab.s[0], tiles_n, tiles_m);
+        gemm_pipe_kernel<WN, WM, TN, TM, UPS, NS, KG, PACKED, BLK><<<tiles_n * tiles_m, threads, 0, s>>>(g, tab.s[0], tiles_n, tiles_m);
     } else {
         SegTable t = tab;
         uint32_t tiles = 0;
@@ -1271,7 +1436,7 @@ static void run_pipe1(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
             t.s[i].tile0 = tiles;
             tiles += (t.s[i].T + BM - 1) / BM;
         }
-        gemm_pipe_grouped_kernel<WN, WM, TN, TM, UPS, NS, KG, PACKED><<<tiles_n * tiles, threads, 0, s>>>(g, t, tiles_n);
+        gemm_pipe_grouped_kernel<WN, WM, TN, TM, UPS, NS, KG, PACKED, BLK><<<tiles_n * tiles, threads, 0, s>>>(g, t, tiles_n);
     }
 }
 
@@ -1286,7 +1451,7 @@ __global__ __launch_bounds__(64 * WN * WM * KG) void gemm_pipe_batch_kernel(JobT
     const uint32_t tiles_n = tab.tiles_n[j];
     uint32_t tn, tm;
     xcd_tile(b, tab.tiles[j], tiles_n, tab.tiles[j] / tiles_n, tn, tm);
-    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, true>(tab.g[j], tab.s[j], tn, tm);
+    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, true, 0>(tab.g[j], tab.s[j], tn, tm);
 }
 
 template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG>
@@ -1304,12 +1469,12 @@ static void run_pipe_batch(const JobTable &jobs, hipStream_t s) {
     gemm_pipe_batch_kernel<WN, WM, TN, TM, UPS, NS, KG><<<wg, 64 * WN * WM * KG, 0, s>>>(t);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG = 1>
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG = 1, int BLK = 0>
 static void run_pipe(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
     if (tab.s[0].qstride)
-        run_pipe1<WN, WM, TN, TM, UPS, NS, KG, true>(g, tab, s);
+        run_pipe1<WN, WM, TN, TM, UPS, NS, KG, true, BLK>(g, tab, s);
     else
-        run_pipe1<WN, WM, TN, TM, UPS, NS, KG, false>(g, tab, s);
+        run_pipe1<WN, WM, TN, TM, UPS, NS, KG, false, BLK>(g, tab, s);
 }
 
 /* The pipelined product's tile shapes: channels x frames, and the units of
@@ -1321,29 +1486,31 @@ struct RingCfg {
     uint32_t kg;                    /* K groups of pipe_tile */
     void (*run)(const GemmArgs &, const SegTable &, hipStream_t);
     void (*batch)(const JobTable &, hipStream_t);   /* pipe_tile only */
+    void (*run64)(const GemmArgs &, const SegTable &, hipStream_t);   /* blocks of 64 inputs, or null */
+    void (*run32)(const GemmArgs &, const SegTable &, hipStream_t);   /* blocks of 32 inputs, or null */
 };
 static const RingCfg kRing[] = {
     /* ring_tile: name <channels x frames, units a stage> */
-    { "ring<128x128,1>", 128, 128, 1, 0, 1, run_ring<2, 2, 4, 4, 1>, nullptr },
-    { "ring<64x64,1>", 64, 64, 1, 0, 1, run_ring<2, 2, 2, 2, 1>, nullptr },
-    { "ring<64x64,2>", 64, 64, 2, 0, 1, run_ring<2, 2, 2, 2, 2>, nullptr },
-    { "ring<64x64,4>", 64, 64, 4, 0, 1, run_ring<2, 2, 2, 2, 4>, nullptr },
+    { "ring<128x128,1>", 128, 128, 1, 0, 1, run_ring<2, 2, 4, 4, 1>, nullptr, nullptr, nullptr },
+    { "ring<64x64,1>", 64, 64, 1, 0, 1, run_ring<2, 2, 2, 2, 1>, nullptr, nullptr, nullptr },
+    { "ring<64x64,2>", 64, 64, 2, 0, 1, run_ring<2, 2, 2, 2, 2>, nullptr, nullptr, nullptr },
+    { "ring<64x64,4>", 64, 64, 4, 0, 1, run_ring<2, 2, 2, 2, 4>, nullptr, nullptr, nullptr },
     /* pipe_tile: name <channels x frames, units a stage, slots>; w8: eight
      * waves of 64 x 32 */
-    { "pipe<128x128,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 2, 4, 4, 1, 4, 1>, run_pipe_batch<2, 2, 4, 4, 1, 4, 1> },
-    { "pipe<128x128w8,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 4, 4, 2, 1, 4, 1>, run_pipe_batch<2, 4, 4, 2, 1, 4, 1> },
-    { "pipe<64x64,2,4>", 64, 64, 2, 4, 1, run_pipe<2, 2, 2, 2, 2, 4, 1>, run_pipe_batch<2, 2, 2, 2, 2, 4, 1> },
-    { "pipe<64x64,4,4>", 64, 64, 4, 4, 1, run_pipe<2, 2, 2, 2, 4, 4, 1>, run_pipe_batch<2, 2, 2, 2, 4, 4, 1> },
+    { "pipe<128x128,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 2, 4, 4, 1, 4, 1>, run_pipe_batch<2, 2, 4, 4, 1, 4, 1>, run_pipe<2, 2, 4, 4, 1, 4, 1, 1>, run_pipe<2, 2, 4, 4, 1, 4, 1, 2> },
+    { "pipe<128x128w8,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 4, 4, 2, 1, 4, 1>, run_pipe_batch<2, 4, 4, 2, 1, 4, 1>, run_pipe<2, 4, 4, 2, 1, 4, 1, 1>, run_pipe<2, 4, 4, 2, 1, 4, 1, 2> },
+    { "pipe<64x64,2,4>", 64, 64, 2, 4, 1, run_pipe<2, 2, 2, 2, 2, 4, 1>, run_pipe_batch<2, 2, 2, 2, 2, 4, 1>, run_pipe<2, 2, 2, 2, 2, 4, 1, 1>, run_pipe<2, 2, 2, 2, 2, 4, 1, 2> },
+    { "pipe<64x64,4,4>", 64, 64, 4, 4, 1, run_pipe<2, 2, 2, 2, 4, 4, 1>, run_pipe_batch<2, 2, 2, 2, 4, 4, 1>, nullptr, nullptr },
     /* eight waves of 64 x 64 */
-    { "pipe<128x256w8,1,4>", 128, 256, 1, 4, 1, run_pipe<2, 4, 4, 4, 1, 4, 1>, run_pipe_batch<2, 4, 4, 4, 1, 4, 1> },
-    { "pipe<128x256w8,1,6>", 128, 256, 1, 6, 1, run_pipe<2, 4, 4, 4, 1, 6, 1>, run_pipe_batch<2, 4, 4, 4, 1, 6, 1> },
-    { "pipe<256x128w8,1,4>", 256, 128, 1, 4, 1, run_pipe<4, 2, 4, 4, 1, 4, 1>, run_pipe_batch<4, 2, 4, 4, 1, 4, 1> },
+    { "pipe<128x256w8,1,4>", 128, 256, 1, 4, 1, run_pipe<2, 4, 4, 4, 1, 4, 1>, run_pipe_batch<2, 4, 4, 4, 1, 4, 1>, nullptr, nullptr },
+    { "pipe<128x256w8,1,6>", 128, 256, 1, 6, 1, run_pipe<2, 4, 4, 4, 1, 6, 1>, run_pipe_batch<2, 4, 4, 4, 1, 6, 1>, nullptr, nullptr },
+    { "pipe<256x128w8,1,4>", 256, 128, 1, 4, 1, run_pipe<4, 2, 4, 4, 1, 4, 1>, run_pipe_batch<4, 2, 4, 4, 1, 4, 1>, nullptr, nullptr },
     /* eight waves of 128 x 64 */
-    { "pipe<256x256w8,1,4>", 256, 256, 1, 4, 1, run_pipe<2, 4, 8, 4, 1, 4, 1>, run_pipe_batch<2, 4, 8, 4, 1, 4, 1> },
+    { "pipe<256x256w8,1,4>", 256, 256, 1, 4, 1, run_pipe<2, 4, 8, 4, 1, 4, 1>, run_pipe_batch<2, 4, 8, 4, 1, 4, 1>, nullptr, nullptr },
     /* two K groups of four waves of 32 x 32 */
-    { "pipe<64x64,2,4,k2>", 64, 64, 2, 4, 2, run_pipe<2, 2, 2, 2, 2, 4, 2>, run_pipe_batch<2, 2, 2, 2, 2, 4, 2> },
-    { "pipe<64x64,1,4,k2>", 64, 64, 1, 4, 2, run_pipe<2, 2, 2, 2, 1, 4, 2>, run_pipe_batch<2, 2, 2, 2, 1, 4, 2> },
-    { "pipe<64x64,2,2,k2>", 64, 64, 2, 2, 2, run_pipe<2, 2, 2, 2, 2, 2, 2>, run_pipe_batch<2, 2, 2, 2, 2, 2, 2> },
+    { "pipe<64x64,2,4,k2>", 64, 64, 2, 4, 2, run_pipe<2, 2, 2, 2, 2, 4, 2>, run_pipe_batch<2, 2, 2, 2, 2, 4, 2>, nullptr, nullptr },
+    { "pipe<64x64,1,4,k2>", 64, 64, 1, 4, 2, run_pipe<2, 2, 2, 2, 1, 4, 2>, run_pipe_batch<2, 2, 2, 2, 1, 4, 2>, nullptr, nullptr },
+    { "pipe<64x64,2,2,k2>", 64, 64, 2, 2, 2, run_pipe<2, 2, 2, 2, 2, 2, 2>, run_pipe_batch<2, 2, 2, 2, 2, 2, 2>, nullptr, nullptr },
 };
 constexpr int kNRing = sizeof kRing / sizeof kRing[0];
 
@@ -1456,6 +1623,20 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
         kRing[c].run(g, tab, s);
         *name = kRing[c].name;
         return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    /* blocks of 64 or 32 inputs (the encoder's modes): the pipelined tile
+     * the heuristic picks for these frames, if it has a blocked variant */
+    if ((mode == 1 && g.qb == 64) || (mode == 2 && g.qb == 32)) {
+        int c = pick_ring(g.rows, frames, g.ku);
+        if (!(mode == 1 ? kRing[c].run64 : kRing[c].run32))
+            c = fits(6, g.ku) ? 6 : 4;      /* 4 takes any ku: one unit a stage, four slots */
+        auto run = mode == 1 ? kRing[c].run64 : kRing[c].run32;
+        if (run) {
+            run(g, tab, s);
+            snprintf(buf, sizeof buf, "%s %s", kRing[c].name, modes[mode]);
+            *name = buf;
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
     }
     /* 128 x 128 tiles where they fill the chip, 64 x 64 where they do not */
     const uint64_t big = (uint64_t)((g.rows + 127) / 128) * ((frames + 127) / 128);

@@ -260,3 +260,63 @@ def test_batch_of_products(hip, torch, K):
         hip.force_tiling(-1)
         for m in mats:
             m.release()
+
+
+@pytest.mark.parametrize("qb", [32, 64])
+@pytest.mark.parametrize("M,K,N", [(750, 1024, 1024), (300, 4096, 1024), (37, 1056, 208), (129, 512, 64),
+                                   (1499, 1024, 96)])
+def test_blocked_products(hip, torch, qb, M, K, N):
+    """The encoder's blocks (qb 32 and 64) on the pipelined tiles: the packed
+    quantize's q, d and packed bytes are the oracle's, and the product of every
+    tiling with a blocked variant, packed and row-major, with bias and add,
+    under each rounding mode, is the oracle's, bit for bit. K = 1056 has an
+    odd number of 32-input blocks and a padding unit past them."""
+    if K % qb:
+        pytest.skip("qb does not divide K")
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    g = synth.rng(M + K + N + qb)
+    w = synth.pack_q8(synth.weights(g, N, K))
+    ws = synth.scales(g, N)
+    bias = g.standard_normal(N).astype(np.float32)
+    x = synth.activations(g, M, K)
+    dev = torch.device("cuda")
+    xt = torch.from_numpy(x).to(dev)
+    qt = torch.empty((M, K), dtype=torch.int8, device=dev)
+    dt = torch.empty((M * K // qb,), dtype=torch.float32, device=dev)
+    qp = torch.zeros((hip.packed_bytes(K, M),), dtype=torch.int8, device=dev)
+    say("blocked quantize", qb, M, K, N)
+    hip.quantize_packed_dev(qt, qp, dt, xt, K, M, K, qb=qb)
+    torch.cuda.synchronize()
+    q, d = ol.quantize(x.reshape(-1), M, K, qb, K)
+    assert np.array_equal(qt.cpu().numpy().reshape(-1), q) and np.array_equal(bits(dt.cpu().numpy()), bits(d))
+    assert np.array_equal(unpack_packed(qp.cpu().numpy(), K, M), q.reshape(M, K))
+    base = g.standard_normal(M * N).astype(np.float32)
+    bt = torch.from_numpy(bias).to(dev)
+    modes = {0: 0, 1: 0x800, 2: 0x400, 3: 0xC00}
+    with hip.Q8Matrix(w, ws) as m:
+        try:
+            for rm in (0, 1, 2):
+                want = base.copy()
+                assert libm.fesetround(modes[rm]) == 0
+                try:
+                    ol.gemm_q8(want, N, w, ws, bias, N, q, d, K, qb, M, 1, threads=16)
+                finally:
+                    libm.fesetround(0)
+                for ti in [-1, 4, 5, 6]:
+                    hip.force_tiling(ti)
+                    for packed in (True, False):
+                        out = torch.from_numpy(base).to(dev)
+                        say("blocked product", qb, M, K, N, rm, ti, packed)
+                        if packed:
+                            hip.gemm_q8_packed_dev(out, N, m, 0, N, m.dev_scales, bt, qp, dt, K, M, 1, rmode=rm,
+                                                   qb=qb)
+                        else:
+                            hip.gemm_q8_dev(out, N, m, 0, N, None, bt, qt, dt, K, qb, M, 1, rmode=rm,
+                                            ws_ptr=m.dev_scales)
+                        torch.cuda.synchronize()
+                        assert hip.last_kernel().startswith("pipe"), hip.last_kernel()
+                        assert np.array_equal(bits(out.cpu().numpy().reshape(-1)), bits(want)), \
+                            (qb, M, K, N, rm, ti, packed, hip.last_kernel())
+        finally:
+            hip.force_tiling(-1)
