@@ -1021,7 +1021,7 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
     constexpr int DB = BLK ? (BM * BPS * 4 + kUnitBytes - 1) / kUnitBytes * kUnitBytes : 0;
     constexpr int SLOT = SLOTU * kUnitBytes + DB;
     static_assert(KG * NS * SLOT <= 160 * 1024, "the slots fit a CU's LDS");
-    static_assert(KG == 1 || (KG - 1) * NW * TN * TM * kUnitBytes <= NS * SLOT, "the partial sums fit a ring");
+    static_assert(KG == 1 || (KG - 1) * NW * TN * TM * kUnitBytes <= KG * NS * SLOT, "the partial sums fit the rings");
     static_assert((UPS & (UPS - 1)) == 0, "a power of two units a stage");
     static_assert(NS * UPS % 2 == 0, "the steady state is whole pairs of sub-steps");
     constexpr int R = TN + TM;
@@ -1543,12 +1543,18 @@ int ring_count() { return kNRing; }
 /* The tile for a product of `frames` frames into `rows` channels: the
  * largest that still gives every CU a workgroup. */
 /* whether tiling i takes ku units a panel: ring_tile runs whole passes of
- * four stages; pipe_tile needs its slots' worth of stages to start */
+ * four stages; pipe_tile needs its slots' worth of stages to start, and its
+ * steady state runs whole passes of max(2, UPS) sub-steps, so with one unit
+ * a stage the stages past the slots' first fill must be even in number (a
+ * pass past them would load a stage beyond the last) */
 static bool fits(int i, uint32_t ku) {
     const RingCfg &c = kRing[i];
     if (c.slots == 0)
         return ku % (4 * c.ups) == 0;
-    return ku % (c.kg * c.ups) == 0 && ku / (c.kg * c.ups) >= c.slots;
+    if (ku % (c.kg * c.ups) != 0)
+        return false;
+    const uint32_t ns = ku / (c.kg * c.ups);
+    return ns >= c.slots && (c.ups > 1 || (ns - c.slots) % 2 == 0);
 }
 
 static int pick_ring(uint32_t rows, uint64_t frames, uint32_t ku) {
