@@ -200,6 +200,12 @@ const char *pk_hip_last_kernel(void);
 int pk_hip_tilings(void);
 int pk_hip_force_tiling(int index);
 
+/* Tests and tuning: forcing the packed quantize's kernel for every later
+ * launch in the process: 0 one wave a column, 1 one workgroup a 16-column
+ * group, -1 the automatic choice by size; returns the one forced before.
+ * Both compute the same bits. */
+int pk_hip_force_quantize(int kind);
+
 #ifdef __cplusplus
 }
 #endif

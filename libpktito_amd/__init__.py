@@ -66,6 +66,7 @@ _SIGS = {
     "pk_hip_last_kernel": (ctypes.c_char_p, []),
     "pk_hip_tilings": (ctypes.c_int, []),
     "pk_hip_force_tiling": (ctypes.c_int, [ctypes.c_int]),
+    "pk_hip_force_quantize": (ctypes.c_int, [ctypes.c_int]),
     "pk_hip_init": (ctypes.c_int, []),
     "pk_hip_upload_q8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32]),
     "pk_hip_release_q8": (ctypes.c_int, [ctypes.c_void_p]),
@@ -144,6 +145,13 @@ def force_tiling(index):
     """Force tiling `index` for every later launch (-1: automatic); returns
     the one forced before."""
     return lib().pk_hip_force_tiling(index)
+
+
+def force_quantize(kind):
+    """Force the packed quantize's kernel for every later launch (0 one wave
+    a column, 1 one workgroup a 16-column group, -1 automatic); returns the
+    one forced before."""
+    return lib().pk_hip_force_quantize(kind)
 
 
 def _ptr(a):

@@ -84,6 +84,10 @@ int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size
 int ring_count();
 int set_ring(int i);
 
+/* The packed quantize's kernel: 0 one wave a column, 1 one workgroup a
+ * group, -1 by size; returns the one forced before. */
+int set_quant_kernel(int kind);
+
 /* One product; table->nseg == 1 for a plain call. */
 int launch_gemm(const GemmArgs &g, const SegTable &table, hipStream_t s, const char **name);
 

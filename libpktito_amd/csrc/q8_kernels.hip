@@ -221,9 +221,6 @@ __global__ __launch_bounds__(256) void quant_any_kernel(int8_t *__restrict__ q, 
     d[i] = dv;
 }
 
-/* A whole column is one block, n <= 4096: one wave a column, four columns a
- * workgroup, each lane CH float4 chunks of it (chunk c of lane l is float4
- * l + 64 c), every load issued before the first is used. */
 /* max of a non-negative int over aligned groups of W lanes (W = 8 or 16), in
  * every lane of the group: DPP quad swaps, half mirror, and mirror for 16 */
 template <int W>
@@ -237,9 +234,57 @@ __device__ __forceinline__ int group_max_nonneg(int v) {
     return v;
 }
 
-/* One wave a column of n <= 4096 inputs, four columns a workgroup. QB == 0:
- * the column is one block; QB == 32 or 64: blocks of QB inputs, each the
- * QB / 4 lanes holding it, reduced within those lanes. */
+__device__ __forceinline__ int mag4(float4 f) {
+    return max(max(mag_bits(f.x), mag_bits(f.y)), max(mag_bits(f.z), mag_bits(f.w)));
+}
+
+/* The scales of a column of n <= 4096 inputs that one wave holds, each lane
+ * CH float4 chunks of it (chunk c of lane l is float4 l + 64 c, zeros past
+ * the column). QB == 0: the column is one block, reduced over the wave;
+ * QB == 32 or 64: chunk c's block of QB inputs, reduced within the QB / 4
+ * lanes holding it. All 64 lanes active. */
+template <int CH, int QB>
+struct WaveScales {
+    static constexpr int NB = QB ? CH : 1;
+    float dv[NB], id[NB];
+    bool zero[NB];
+
+    __device__ __forceinline__ void block(int b, uint32_t mb) {
+        zero[b] = zero_bits(mb);
+        dv[b] = 0.0f;
+        id[b] = 0.0f;
+        if (!zero[b]) {
+            const float amax = __uint_as_float(mb);
+            dv[b] = amax / 127.0f;
+            id[b] = 127.0f / amax;
+        }
+    }
+
+    __device__ __forceinline__ explicit WaveScales(const float4 (&v)[CH]) {
+        if constexpr (QB == 0) {
+            int m = 0;
+#pragma unroll
+            for (int c = 0; c < CH; c++)
+                m = max(m, mag4(v[c]));
+            block(0, (uint32_t)wave_max_nonneg(m));
+        } else {
+#pragma unroll
+            for (int c = 0; c < CH; c++)
+                block(c, (uint32_t)group_max_nonneg<QB / 4>(mag4(v[c])));
+        }
+    }
+};
+
+/* Where inputs k..k+3 of frame r of a 16-frame group sit in the group's
+ * unit k / 64: at 16 (16 kq + r) + k % 16, kq = (k % 64) / 16. Unit u of
+ * group g is unit u G + g of the packed copy of G groups. */
+__device__ __forceinline__ uint32_t in_unit(uint32_t k, uint32_t r) {
+    return (((k >> 4) & 3) * 16 + r) * 16 + (k & 15);
+}
+
+/* One wave a column of n <= 4096 inputs, four columns a workgroup (the
+ * quantizes of up to about 7M inputs, where the kernel is one memory round
+ * trip and wants its loads spread over the most CUs). */
 template <int CH, bool PACK, int QB>
 __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q, int8_t *__restrict__ qp,
                                                          float *__restrict__ d, const float *__restrict__ x,
@@ -256,85 +301,120 @@ __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q,
         const uint32_t i = lane + 64 * c;
         v[c] = i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    auto mag4 = [](float4 f) {
-        return max(max(mag_bits(f.x), mag_bits(f.y)), max(mag_bits(f.z), mag_bits(f.w)));
-    };
-    /* the scale of each chunk's block: one for the column, or one a chunk */
-    float dv[QB ? CH : 1], id[QB ? CH : 1];
-    bool zero[QB ? CH : 1];
-    if constexpr (QB == 0) {
-        int m = 0;
-#pragma unroll
-        for (int c = 0; c < CH; c++)
-            m = max(m, mag4(v[c]));
-        const uint32_t mb = (uint32_t)wave_max_nonneg(m);
-        zero[0] = zero_bits(mb);
-        dv[0] = 0.0f;
-        id[0] = 0.0f;
-        if (!zero[0]) {
-            const float amax = __uint_as_float(mb);
-            dv[0] = amax / 127.0f;
-            id[0] = 127.0f / amax;
-        }
-    } else {
-#pragma unroll
-        for (int c = 0; c < CH; c++) {
-            const uint32_t mb = (uint32_t)group_max_nonneg<QB / 4>(mag4(v[c]));
-            zero[c] = zero_bits(mb);
-            dv[c] = 0.0f;
-            id[c] = 0.0f;
-            if (!zero[c]) {
-                const float amax = __uint_as_float(mb);
-                dv[c] = amax / 127.0f;
-                id[c] = 127.0f / amax;
-            }
-        }
-    }
+    const WaveScales<CH, QB> sc(v);
     int *qr = (int *)(q + (size_t)t * n);
-    /* packed: row t is row t % 16 of group t / 16; inputs k..k+3 of unit
-     * k / 64 sit at 16 (16 kq + r) + k % 16, kq = (k % 64) / 16 */
     const uint32_t G = (T + 15) / 16, g = t >> 4, r = t & 15;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
         const int cb = QB ? c : 0;
         if (i < n4) {
-            const int v4 = zero[cb] ? 0 : pack4(v[c], id[cb]);
+            const int v4 = sc.zero[cb] ? 0 : pack4(v[c], sc.id[cb]);
             if (!PACK || q)
                 qr[i] = v4;
             if (PACK) {
-                const uint32_t k = 4 * i, u = k >> 6, kq = (k >> 4) & 3;
-                *(int *)(qp + ((size_t)u * G + g) * kUnitBytes + (kq * 16 + r) * 16 + (k & 15)) = v4;
+                const uint32_t k = 4 * i;
+                *(int *)(qp + ((size_t)(k >> 6) * G + g) * kUnitBytes + in_unit(k, r)) = v4;
             }
             if (QB && (i & (QB / 4 - 1)) == 0)
-                d[(size_t)t * (n / QB) + (4 * i) / QB] = dv[cb];
+                d[(size_t)t * (n / QB) + (4 * i) / QB] = sc.dv[cb];
         }
     }
     if (QB == 0 && lane == 0)
-        d[t] = dv[0];
+        d[t] = sc.dv[0];
+}
+
+/* One workgroup of 16 waves a group of 16 columns, for the packed copy of
+ * about 7M inputs and more: wave r quantizes column 16 g + r as
+ * quant_wave_kernel does, the group's units are put together in LDS, and
+ * each unit leaves as one contiguous 1 KB of 16-byte stores (measured on
+ * inputs the caches no longer hold: 10% sooner than the 4-byte stores at
+ * these sizes, which are bound by HBM). The stores are ordinary ones: the
+ * product that reads the copy next finds it in the memory-side cache, and
+ * a layer of ten minutes of audio took 2% longer with non-temporal stores.
+ * Columns past T are written as zero rows of the group. */
+template <int CH, int QB>
+__global__ __launch_bounds__(1024) void quant_group_kernel(int8_t *__restrict__ q, int8_t *__restrict__ qp,
+                                                           float *__restrict__ d, const float *__restrict__ x,
+                                                           size_t xs, uint32_t n, uint32_t T) {
+    __shared__ __attribute__((aligned(16))) int8_t units[CH * 4 * kUnitBytes];
+    const int lane = threadIdx.x & 63, r = threadIdx.x >> 6;
+    const uint32_t g = blockIdx.x, G = gridDim.x, t = 16 * g + r;
+    const uint32_t n4 = n >> 2, nw = 16 * ((n + 63) / 64);     /* 4-byte words a frame's units hold */
+    const bool live = t < T;
+    const float4 *xr = (const float4 *)(x + (size_t)(live ? t : 0) * xs);
+    float4 v[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        v[c] = live && i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const WaveScales<CH, QB> sc(v);
+    int *qr = (int *)(q + (size_t)t * n);
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        const int cb = QB ? c : 0;
+        if (i < nw) {
+            const bool in = live && i < n4;
+            const int v4 = !in || sc.zero[cb] ? 0 : pack4(v[c], sc.id[cb]);
+            *(int *)(units + (i >> 4) * kUnitBytes + in_unit(4 * i, r)) = v4;
+            if (in && q)
+                qr[i] = v4;
+            if (QB && in && (i & (QB / 4 - 1)) == 0)
+                d[(size_t)t * (n / QB) + (4 * i) / QB] = sc.dv[cb];
+        }
+    }
+    if (QB == 0 && live && lane == 0)
+        d[t] = sc.dv[0];
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < 4 * nw; j += 1024) {
+        const uint32_t u = j >> 6;
+        const v4i val = *(const v4i *)(units + 16 * j);
+        *(v4i *)(qp + ((size_t)u * G + g) * kUnitBytes + 16 * (j & 63)) = val;
+    }
+}
+
+/* The packed quantize's kernel by size: one wave a column below about 7M
+ * inputs, one workgroup a group from there (the crossover measured on
+ * inputs the caches no longer hold: 6.1M inputs are sooner the first way,
+ * 7.7M the second). */
+constexpr uint64_t kGroupQuantInputs = 7ull << 20;
+static int g_quant_kernel = -1;
+
+int set_quant_kernel(int kind) {
+    const int was = g_quant_kernel;
+    g_quant_kernel = kind < 0 || kind > 1 ? -1 : kind;
+    return was;
 }
 
 int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
                            uint32_t qb, uint32_t T, hipStream_t s, const char **name) {
     if (T == 0)
         return 0;
-    const uint32_t n4 = n / 4, grid4 = (T + 3) / 4;
+    const uint32_t n4 = n / 4;
     if (n4 > 1024 || !(qb == n || qb == 32 || qb == 64))
         return -2;
     const bool small = n4 <= 256;
-#define PK_QW(CH, QB, NAME)                                                          \
-    do {                                                                             \
-        quant_wave_kernel<CH, true, QB><<<grid4, 256, 0, s>>>(q, qp, d, x, xs, n, T); \
-        *name = NAME;                                                                \
+    const bool group = g_quant_kernel < 0 ? (uint64_t)T * n >= kGroupQuantInputs : g_quant_kernel == 1;
+#define PK_QP(CH, QB, NAME)                                                                       \
+    do {                                                                                          \
+        if (group) {                                                                              \
+            quant_group_kernel<CH, QB><<<(T + 15) / 16, 1024, 0, s>>>(q, qp, d, x, xs, n, T);    \
+            *name = "quant_group_packed" NAME;                                                    \
+        } else {                                                                                  \
+            quant_wave_kernel<CH, true, QB><<<(T + 3) / 4, 256, 0, s>>>(q, qp, d, x, xs, n, T);  \
+            *name = "quant_wave_packed" NAME;                                                     \
+        }                                                                                         \
     } while (0)
     if (qb == n) {
-        if (small) PK_QW(4, 0, "quant_wave_packed<4>"); else PK_QW(16, 0, "quant_wave_packed<16>");
+        if (small) PK_QP(4, 0, "<4>"); else PK_QP(16, 0, "<16>");
     } else if (qb == 32) {
-        if (small) PK_QW(4, 32, "quant_wave_packed<4,qb32>"); else PK_QW(16, 32, "quant_wave_packed<16,qb32>");
+        if (small) PK_QP(4, 32, "<4,qb32>"); else PK_QP(16, 32, "<16,qb32>");
     } else {
-        if (small) PK_QW(4, 64, "quant_wave_packed<4,qb64>"); else PK_QW(16, 64, "quant_wave_packed<16,qb64>");
+        if (small) PK_QP(4, 64, "<4,qb64>"); else PK_QP(16, 64, "<16,qb64>");
     }
-#undef PK_QW
+#undef PK_QP
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -320,3 +320,52 @@ def test_blocked_products(hip, torch, qb, M, K, N):
                             (qb, M, K, N, rm, ti, packed, hip.last_kernel())
         finally:
             hip.force_tiling(-1)
+
+
+def special_rows(x):
+    """Columns the block rule zeroes or scales at its edges: all zeros, a NaN,
+    an infinity, every magnitude below 2^-121 (zeroed), and a largest
+    magnitude of exactly 2^-121 (kept, with a subnormal scale)."""
+    T, n = x.shape
+    if T >= 6:
+        x[1] = 0.0
+        x[2, n // 2] = np.nan
+        x[3, n - 1] = -np.inf
+        x[4] = np.sign(x[4]) * np.float32(2.0 ** -122)
+        x[5] = x[5] * np.float32(2.0 ** -125)
+        x[5, 7] = np.float32(2.0 ** -121)
+    return x
+
+
+@pytest.mark.parametrize("T,n,qb", [(1, 32, 32), (5, 640, 640), (97, 608, 608), (97, 1056, 32), (17, 4096, 64),
+                                    (300, 4096, 4096), (300, 4096, 64), (750, 1024, 32), (2000, 4096, 4096),
+                                    (1800, 4096, 32), (7500, 1024, 1024), (2249, 4096, 64)])
+def test_packed_quantize_kernels(hip, torch, T, n, qb):
+    """Both packed quantize kernels (one wave a column; one workgroup a
+    16-column group) and the choice by size: q, d and the packed bytes are
+    the oracle's, with and without the row-major copy, over a packed buffer
+    that held other bytes before."""
+    g = synth.rng(T * 7 + n + qb)
+    x = special_rows(synth.activations(g, T, n))
+    q, d = ol.quantize(x.reshape(-1), T, n, qb, n)
+    dev = torch.device("cuda")
+    xt = torch.from_numpy(x).to(dev)
+    big = T * n >= 7 << 20
+    try:
+        for kind in (-1, 0, 1):
+            hip.force_quantize(kind)
+            for with_q in (True, False):
+                qt = torch.full((T, n), 77, dtype=torch.int8, device=dev) if with_q else None
+                dt = torch.full((T * n // qb,), 5.0, dtype=torch.float32, device=dev)
+                qp = torch.full((hip.packed_bytes(n, T),), -3, dtype=torch.int8, device=dev)
+                say("packed quantize", T, n, qb, kind, with_q)
+                hip.quantize_packed_dev(qt, qp, dt, xt, n, T, n, qb=qb)
+                torch.cuda.synchronize()
+                want = "quant_group" if kind == 1 or (kind == -1 and big) else "quant_wave"
+                assert hip.last_kernel().startswith(want), (kind, hip.last_kernel())
+                if with_q:
+                    assert np.array_equal(qt.cpu().numpy().reshape(-1), q)
+                assert np.array_equal(bits(dt.cpu().numpy()), bits(d))
+                assert np.array_equal(unpack_packed(qp.cpu().numpy(), n, T), q.reshape(T, n))
+    finally:
+        hip.force_quantize(-1)
