@@ -188,6 +188,79 @@ typedef struct {
  * device pointers throughout. */
 int pk_hip_gemm_q8_batch_dev(const pk_hip_job *jobs, uint32_t njobs, int rmode, void *stream);
 
+/* ----------------------------------------- the device-resident layer --- */
+
+/* The producers of the encoder's activations (core/encoder.c), each fused
+ * with the quantize that follows it there and writing the packed copy qp
+ * (pk_hip_packed_bytes(a->n, a->T) long) and a->d that the next product
+ * reads; a->q is not written. Device pointers, 16-byte aligned; a->qb the
+ * whole row, 32 or 64 (dwq: 32 or 64). Same bits as the reference's pass
+ * followed by its quantize. No counterpart in the reference's kernel table:
+ * these are its CPU passes between the products (core/encoder.c:108-176),
+ * which a device-resident caller runs where the activations already are. */
+
+/* normq (core/encoder.c:108-128): each of a->T frames of a->n floats at x
+ * (frame t at x + t a->n) layer-normed by w, b, eps (backend/kernels.h:
+ * 112-122) and quantized; a->n a multiple of 64 up to 4096. */
+int pk_hip_normq_dev(pk_hip_act *a, int8_t *qp, const float *x, const float *w, const float *b, float eps,
+                     void *stream);
+
+/* siluq (core/encoder.c:130-156): SiLU of each frame (stride xs) then the
+ * quantize; a->n a multiple of 32 up to 4096. */
+int pk_hip_siluq_dev(pk_hip_act *a, int8_t *qp, const float *x, size_t xs, void *stream);
+
+/* dw (core/encoder.c:158-176): GLU of u [T][2 a->n] (backend/kernels.h:
+ * 140-142), the depthwise convolution of K <= 33 taps w [a->n][K] with bias
+ * b and SiLU (backend/kernels.h:144-158), quantized; a->n a multiple of 64. */
+int pk_hip_dwq_dev(pk_hip_act *a, int8_t *qp, const float *u, const float *w, const float *b, uint32_t K,
+                   void *stream);
+
+/* The layer norm in place over T rows of n floats (backend/kernels.h:
+ * 112-122; core/encoder.c:86-99); n a multiple of 64 up to 4096. */
+int pk_hip_layernorm_dev(float *x, uint32_t T, uint32_t n, const float *w, const float *b, float eps,
+                         void *stream);
+
+/* The attention's float part (core/encoder.c:280-327): H heads of D / H
+ * dimensions (a multiple of 64), o [T][D] from the products' outputs q, k,
+ * v [T][D] and the positions' p [2T - 1][D] with the biases u and v [D]:
+ * Transformer-XL's scores, the softmax, the weighted values, each output
+ * the chain pk_k_gemm_f32 and pk_k_softmax make. The scores live in ws,
+ * pk_hip_attention_workspace(T, H) bytes. */
+size_t pk_hip_attention_workspace(uint32_t T, uint32_t H);
+int pk_hip_attention_dev(float *o, const float *q, const float *k, const float *v, const float *p,
+                         const float *bias_u, const float *bias_v, uint32_t T, uint32_t D, uint32_t H, void *ws,
+                         size_t ws_bytes, void *stream);
+
+/* One encoder layer's weights on the device (core/model.h:45-53): the
+ * eleven matrices uploaded, the vectors as device pointers. D = d_model
+ * (a multiple of 64 up to 4096), H heads of D / H (a multiple of 64),
+ * F = ff_dim (a multiple of 64 up to 4096), K depthwise taps (<= 33). */
+typedef struct {
+    uint32_t D, H, F, K;
+    float    eps;
+    const float *ff1_nw, *ff1_nb, *att_nw, *att_nb, *conv_nw, *conv_nb;
+    const float *ff2_nw, *ff2_nb, *out_nw, *out_nb;
+    const pk_hip_q8 *ff1_up, *ff1_down, *ff2_up, *ff2_down;
+    const pk_hip_q8 *q, *k, *v, *pos, *o;
+    const float *bias_u, *bias_v;
+    const pk_hip_q8 *pw1, *pw2;
+    const float *dw, *dw_b;
+} pk_hip_layer;
+
+/* Bytes of device workspace pk_hip_layer_dev needs at T frames. */
+size_t pk_hip_layer_workspace(const pk_hip_layer *L, uint32_t T, uint32_t qb);
+
+/* One layer (core/encoder.c:321-368) in place on x [T][D] in HBM: the
+ * positions' activations ape_qp / ape_d are 2T - 1 frames of D quantized in
+ * blocks of qb (pk_hip_quantize_packed_dev once an encode, core/encoder.c:
+ * 467-469); the layer's activations are quantized in blocks of qb (32 or
+ * 64, the encoder's modes, core/encoder.c:50-56). Every kernel on stream,
+ * nothing allocated: ws is ws_bytes >= pk_hip_layer_workspace(L, T, qb) of
+ * device memory. The same bits as the reference's layer() over its ref
+ * kernels. Calls that overlap on one workspace race. */
+int pk_hip_layer_dev(const pk_hip_layer *L, float *x, uint32_t T, const int8_t *ape_qp, const float *ape_d,
+                     uint32_t qb, void *ws, size_t ws_bytes, void *stream);
+
 /* The kernel variant the calling thread launched last, for profiling and
  * tests. */
 const char *pk_hip_last_kernel(void);

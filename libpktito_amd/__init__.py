@@ -57,6 +57,22 @@ class Job(ctypes.Structure):
                 ("bias", ctypes.c_void_p), ("a", Act), ("qp", ctypes.c_void_p), ("add", ctypes.c_int)]
 
 
+_F32P = ctypes.c_void_p
+LAYER_VECTORS = ("ff1_nw", "ff1_nb", "att_nw", "att_nb", "conv_nw", "conv_nb", "ff2_nw", "ff2_nb", "out_nw",
+                 "out_nb")
+LAYER_MATRICES = ("ff1_up", "ff1_down", "ff2_up", "ff2_down", "q", "k", "v", "pos", "o", "pw1", "pw2")
+
+
+class LayerW(ctypes.Structure):
+    """pk_hip_layer: one encoder layer's weights on the device (core/model.h:45-53)."""
+    _fields_ = ([("D", ctypes.c_uint32), ("H", ctypes.c_uint32), ("F", ctypes.c_uint32), ("K", ctypes.c_uint32),
+                 ("eps", ctypes.c_float)] + [(n, _F32P) for n in LAYER_VECTORS] +
+                [(n, ctypes.c_void_p) for n in ("ff1_up", "ff1_down", "ff2_up", "ff2_down", "q", "k", "v", "pos",
+                                                "o")] +
+                [("bias_u", _F32P), ("bias_v", _F32P), ("pw1", ctypes.c_void_p), ("pw2", ctypes.c_void_p),
+                 ("dw", _F32P), ("dw_b", _F32P)])
+
+
 _lib = None
 
 # every function include/pk_hip.h declares, with its ctypes signature
@@ -94,6 +110,21 @@ _SIGS = {
                                                   ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]),
     "pk_hip_gemm_q8_batch_dev": (ctypes.c_int, [ctypes.POINTER(Job), ctypes.c_uint32, ctypes.c_int,
                                                 ctypes.c_void_p]),
+    "pk_hip_normq_dev": (ctypes.c_int, [ctypes.POINTER(Act), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p]),
+    "pk_hip_siluq_dev": (ctypes.c_int, [ctypes.POINTER(Act), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                        ctypes.c_void_p]),
+    "pk_hip_dwq_dev": (ctypes.c_int, [ctypes.POINTER(Act), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]),
+    "pk_hip_layernorm_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p]),
+    "pk_hip_attention_workspace": (ctypes.c_size_t, [ctypes.c_uint32, ctypes.c_uint32]),
+    "pk_hip_attention_dev": (ctypes.c_int, [ctypes.c_void_p] * 7 + [ctypes.c_uint32] * 3 +
+                             [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "pk_hip_layer_workspace": (ctypes.c_size_t, [ctypes.POINTER(LayerW), ctypes.c_uint32, ctypes.c_uint32]),
+    "pk_hip_layer_dev": (ctypes.c_int, [ctypes.POINTER(LayerW), ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_size_t,
+                                        ctypes.c_void_p]),
 }
 
 
@@ -287,3 +318,79 @@ def gemm_q8_batch_dev(jobs, rmode=0, stream=None):
         arr[i] = Job(_dptr(out), os_, m.handle, r0, rows, ws_ptr, _dptr(bias), Act(None, _dptr(d), n, n, T),
                      _dptr(qp), int(add))
     _check(lib().pk_hip_gemm_q8_batch_dev(arr, len(jobs), int(rmode), _stream(stream)))
+
+
+# ----------------------------------------------- the device-resident layer ---
+
+def normq_dev(qp, d, x, n, qb, T, w, b, eps, stream=None):
+    """normq (core/encoder.c:108-128) on device tensors: T frames of n at x,
+    layer-normed by w, b, eps, quantized in blocks of qb into qp and d."""
+    a = Act(None, _dptr(d), n, qb, T)
+    _check(lib().pk_hip_normq_dev(ctypes.byref(a), _dptr(qp), _dptr(x), _dptr(w), _dptr(b), eps, _stream(stream)))
+
+
+def siluq_dev(qp, d, x, n, qb, T, xs, stream=None):
+    """SiLU then the quantize (core/encoder.c:130-156) on device tensors."""
+    a = Act(None, _dptr(d), n, qb, T)
+    _check(lib().pk_hip_siluq_dev(ctypes.byref(a), _dptr(qp), _dptr(x), xs, _stream(stream)))
+
+
+def dwq_dev(qp, d, u, n, qb, T, w, b, K, stream=None):
+    """GLU of u [T, 2n], the depthwise convolution w [n, K] + b with SiLU,
+    quantized (core/encoder.c:158-176)."""
+    a = Act(None, _dptr(d), n, qb, T)
+    _check(lib().pk_hip_dwq_dev(ctypes.byref(a), _dptr(qp), _dptr(u), _dptr(w), _dptr(b), K, _stream(stream)))
+
+
+def layernorm_dev(x, T, n, w, b, eps, stream=None):
+    """The layer norm in place over T rows of n floats."""
+    _check(lib().pk_hip_layernorm_dev(_dptr(x), T, n, _dptr(w), _dptr(b), eps, _stream(stream)))
+
+
+def attention_workspace(T, H):
+    return lib().pk_hip_attention_workspace(T, H)
+
+
+def attention_dev(o, q, k, v, p, bias_u, bias_v, T, D, H, ws, stream=None):
+    """The attention's float part (core/encoder.c:280-327) on device tensors;
+    ws a uint8 tensor of attention_workspace(T, H) bytes."""
+    _check(lib().pk_hip_attention_dev(_dptr(o), _dptr(q), _dptr(k), _dptr(v), _dptr(p), _dptr(bias_u),
+                                      _dptr(bias_v), T, D, H, _dptr(ws), ws.numel(), _stream(stream)))
+
+
+class DeviceLayer:
+    """One encoder layer's weights in HBM: the eleven matrices uploaded
+    (Q8Matrix), the vectors as device tensors. weights is a dict of numpy
+    arrays: each of LAYER_VECTORS, bias_u, bias_v, dw [D, K], dw_b, and for
+    each of LAYER_MATRICES the PK_Q8 bytes `name` and row scales `name_s`;
+    and the shapes D, H, F, K and eps."""
+
+    def __init__(self, weights, torch):
+        dev = torch.device("cuda")
+        self.D, self.H, self.F, self.K = (int(weights[k]) for k in ("D", "H", "F", "K"))
+        self.st = LayerW(D=self.D, H=self.H, F=self.F, K=self.K, eps=float(weights["eps"]))
+        self.tensors = {}
+        for n in LAYER_VECTORS + ("bias_u", "bias_v", "dw", "dw_b"):
+            t = torch.from_numpy(np.ascontiguousarray(weights[n], dtype=np.float32)).to(dev)
+            self.tensors[n] = t
+            setattr(self.st, n, t.data_ptr())
+        self.mats = {}
+        for n in LAYER_MATRICES:
+            m = Q8Matrix(np.ascontiguousarray(weights[n], dtype=np.int8),
+                         np.ascontiguousarray(weights[n + "_s"], dtype=np.float32))
+            self.mats[n] = m
+            setattr(self.st, n, m.handle)
+
+    def workspace(self, T, qb):
+        return lib().pk_hip_layer_workspace(ctypes.byref(self.st), T, qb)
+
+    def run(self, x, T, ape_qp, ape_d, qb, ws, stream=None):
+        """One layer in place on the device tensor x [T, D]; ws a uint8 tensor
+        of at least workspace(T, qb) bytes."""
+        _check(lib().pk_hip_layer_dev(ctypes.byref(self.st), _dptr(x), T, _dptr(ape_qp), _dptr(ape_d), qb,
+                                      _dptr(ws), ws.numel(), _stream(stream)))
+
+    def release(self):
+        for m in self.mats.values():
+            m.release()
+        self.mats = {}

@@ -1,0 +1,449 @@
+/* The float kernels of the device-resident encoder layer: the producers that
+ * make the int8 products' activations in place of the reference's fused CPU
+ * passes (core/encoder.c:108-176 in peterheb/libpktito: normq, siluq_tile,
+ * dw_item) and the attention's float products (core/encoder.c:280-327,
+ * att_item), so that a layer's activations never leave HBM.
+ *
+ * Bits. Each output is the reference's ref backend's (backend/ref/
+ * kernels.c:90-176): every sum the reference chains in order is one chain in
+ * one lane here, in the same order (a row's 16 lane sums and their tree, a
+ * float product's fmaf chain over its inputs, the depthwise taps); what is
+ * order-free (a max, an elementwise function) is computed in whatever order
+ * the lanes hold it. exp and sigmoid are the reference's own (q8_device.h).
+ * Built with -ffp-contract=off; divisions and square roots are IEEE.
+ */
+#include "q8_device.h"
+#include "q8_internal.h"
+
+#include <math.h>
+
+#pragma clang fp contract(off)
+
+namespace pkq8 {
+
+/* ---------------------------------------------------------- row sums --
+ *
+ * backend/kernels.h:105-110: a row's sum in 16 lanes, element i into lane
+ * i % 16 in order, the lanes combined as acc[i] += acc[i + h] for h = 8, 4,
+ * 2, 1. Here lane l of each 16-lane group holds acc[l]; the tree is the same
+ * additions (a + b is b + a in IEEE arithmetic), the sum lands in the
+ * group's lane 0 and is broadcast to the group. */
+__device__ __forceinline__ float lanes16_sum(float v) {
+    v = v + __shfl_down(v, 8, 16);
+    v = v + __shfl_down(v, 4, 16);
+    v = v + __shfl_down(v, 2, 16);
+    v = v + __shfl_down(v, 1, 16);
+    return __shfl(v, 0, 16);
+}
+
+/* The mean and 1 / sqrt(var + eps) of the row x[0, n) (n a multiple of 16)
+ * as backend/ref/kernels.c:115-129 computes them, in every lane of a 16-lane
+ * group whose lane l is l. */
+__device__ __forceinline__ void row_stats(const float *__restrict__ x, uint32_t n, float eps, uint32_t l,
+                                          float &mean, float &r) {
+    float acc = 0.0f;
+#pragma unroll 8
+    for (uint32_t j = l; j < n; j += 16)
+        acc += x[j];
+    mean = lanes16_sum(acc) / (float)n;
+    acc = 0.0f;
+#pragma unroll 8
+    for (uint32_t j = l; j < n; j += 16) {
+        const float c = x[j] - mean;
+        acc += c * c;
+    }
+    const float var = lanes16_sum(acc) / (float)n;
+    r = 1.0f / sqrtf(var + eps);
+}
+
+/* (v - mean) * r * w + b, left to right (backend/ref/kernels.c:130) */
+__device__ __forceinline__ float4 normed(float4 v, float mean, float r, float4 w, float4 b) {
+    return make_float4((v.x - mean) * r * w.x + b.x, (v.y - mean) * r * w.y + b.y, (v.z - mean) * r * w.z + b.z,
+                       (v.w - mean) * r * w.w + b.w);
+}
+
+/* ------------------------------------------------------------- normq --
+ *
+ * core/encoder.c:108-128: each frame layer-normed and quantized whole, in
+ * blocks of QB (0: the whole row), into the packed copy and d. One wave a
+ * frame, four frames a workgroup. The row's sums take 16 lanes (their
+ * chains are the reference's and cannot be split); the wave's other lanes
+ * compute the same chains, which costs nothing on the critical path. Then
+ * each lane takes float4 chunks i + 64 c of the row, as the quantizer does. */
+template <int CH, int QB>
+__global__ __launch_bounds__(256) void normq_kernel(int8_t *__restrict__ qp, float *__restrict__ d,
+                                                    const float *__restrict__ x, uint32_t n, uint32_t T,
+                                                    const float *__restrict__ w, const float *__restrict__ b,
+                                                    float eps) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T)
+        return;
+    const float *xr = x + (size_t)t * n;
+    float mean, r;
+    row_stats(xr, n, eps, lane & 15, mean, r);
+    const uint32_t n4 = n >> 2;
+    float4 v[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        v[c] = i < n4 ? normed(((const float4 *)xr)[i], mean, r, ((const float4 *)w)[i], ((const float4 *)b)[i])
+                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const WaveScales<CH, QB> sc(v);
+    const uint32_t G = (T + 15) / 16, g = t >> 4, fr = t & 15;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        const int cb = QB ? c : 0;
+        if (i < n4) {
+            const uint32_t k = 4 * i;
+            *(int *)(qp + ((size_t)(k >> 6) * G + g) * kUnitBytes + in_unit(k, fr)) =
+                sc.zero[cb] ? 0 : pack4(v[c], sc.id[cb]);
+            if (QB && (i & (QB / 4 - 1)) == 0)
+                d[(size_t)t * (n / QB) + k / QB] = sc.dv[cb];
+        }
+    }
+    if (QB == 0 && lane == 0)
+        d[t] = sc.dv[0];
+}
+
+/* core/encoder.c:86-99 (norm): the layer's last layer norm, in place. */
+template <int CH>
+__global__ __launch_bounds__(256) void norm_kernel(float *__restrict__ x, uint32_t n, uint32_t T,
+                                                   const float *__restrict__ w, const float *__restrict__ b,
+                                                   float eps) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T)
+        return;
+    float *xr = x + (size_t)t * n;
+    float mean, r;
+    row_stats(xr, n, eps, lane & 15, mean, r);
+    const uint32_t n4 = n >> 2;
+    float4 v[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < n4)
+            v[c] = normed(((const float4 *)xr)[i], mean, r, ((const float4 *)w)[i], ((const float4 *)b)[i]);
+    }
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < n4)
+            ((float4 *)xr)[i] = v[c];
+    }
+}
+
+/* ---------------------------------------------------------- attention --
+ *
+ * core/encoder.c:280-327, per head h of dk dimensions, query i, key j:
+ *   score(i, j) = chain_d fmaf(k_j[d], q_i[d] + u[d])
+ *               + chain_d fmaf(p_{T-1-i+j}[d], q_i[d] + v[d])
+ * each chain over d = 0 .. dk-1 in order from +0 (pk_k_gemm_f32), the two
+ * added once; softmax over the T keys (pk_k_softmax: the scale, the max,
+ * pk_expf, the 16-lane sum, one division); then
+ *   o(i, d) = chain_j fmaf(v_j[d], P(i, j))  over j = 0 .. T-1 in order.
+ * The reference lays K, P and V out as panels for its CPU kernel; the bits
+ * depend only on each output's chain, so the products' row-major outputs
+ * are read as they are.
+ *
+ * Three kernels: the scores of 64 x 64 (query, key) tiles, each thread a
+ * 4 x 4 of them (queries ti + 16a, keys tj + 16b) with the head's
+ * dimensions staged through LDS 32 at a time (queries with each bias,
+ * keys, and the 127 position rows the tile's diagonals reach); the
+ * softmax of each row in 16 lanes; and the weighted sum of the values,
+ * 32 queries x 64 dimensions a workgroup, keys staged 32 at a time. */
+constexpr int kAT = 64;     /* queries and keys a score tile */
+constexpr int kADC = 32;    /* dimensions a stage */
+
+__global__ __launch_bounds__(256) void att_scores_kernel(float *__restrict__ S, uint32_t Ts,
+                                                         const float *__restrict__ qf,
+                                                         const float *__restrict__ kf,
+                                                         const float *__restrict__ pf,
+                                                         const float *__restrict__ bu,
+                                                         const float *__restrict__ bv, uint32_t T, uint32_t D,
+                                                         uint32_t dk) {
+    __shared__ float squ[kAT][kADC + 1], sqv[kAT][kADC + 1], sk[kAT][kADC + 1], sp[2 * kAT - 1][kADC + 1];
+    const uint32_t j0 = blockIdx.x * kAT, i0 = blockIdx.y * kAT, h = blockIdx.z;
+    const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
+    const uint32_t R = 2 * T - 1;
+    /* position row of local row 0: T - 1 - (i0 + 63) + j0 */
+    const int64_t m0 = (int64_t)T - 1 - (int64_t)i0 - (kAT - 1) + (int64_t)j0;
+    float sc[4][4], bd[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+            sc[a][b] = bd[a][b] = 0.0f;
+    for (uint32_t d0 = 0; d0 < dk; d0 += kADC) {
+        const uint32_t col = h * dk + d0;
+        for (int e = tid; e < kAT * kADC; e += 256) {
+            const int r = e / kADC, c = e % kADC;
+            const uint32_t i = i0 + r, j = j0 + r;
+            const float q = i < T ? qf[(size_t)i * D + col + c] : 0.0f;
+            squ[r][c] = q + bu[col + c];
+            sqv[r][c] = q + bv[col + c];
+            sk[r][c] = j < T ? kf[(size_t)j * D + col + c] : 0.0f;
+        }
+        for (int e = tid; e < (2 * kAT - 1) * kADC; e += 256) {
+            const int r = e / kADC, c = e % kADC;
+            const int64_t m = m0 + r;
+            sp[r][c] = m >= 0 && m < (int64_t)R ? pf[(size_t)m * D + col + c] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int c = 0; c < kADC; c++) {
+            float qu[4], qv[4], kk[4], pp[7];
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                qu[a] = squ[ti + 16 * a][c];
+                qv[a] = sqv[ti + 16 * a][c];
+                kk[a] = sk[tj + 16 * a][c];
+            }
+            /* query ti + 16a against key tj + 16b reads local position row
+             * 63 - ti + tj + 16 (b - a) */
+#pragma unroll
+            for (int e = 0; e < 7; e++)
+                pp[e] = sp[kAT - 1 - ti + tj + 16 * (e - 3)][c];
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    sc[a][b] = __builtin_fmaf(kk[b], qu[a], sc[a][b]);
+                    bd[a][b] = __builtin_fmaf(pp[b - a + 3], qv[a], bd[a][b]);
+                }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint32_t i = i0 + ti + 16 * a, j = j0 + tj + 16 * b;
+            if (i < T && j < T)
+                S[((size_t)h * T + i) * Ts + j] = sc[a][b] + bd[a][b];
+        }
+}
+
+/* backend/ref/kernels.c:134-147 on rows of T scores, 16 lanes a row:
+ * lane l takes keys l, l + 16, ... in order. */
+__global__ __launch_bounds__(256) void att_softmax_kernel(float *__restrict__ S, uint32_t Ts, uint32_t rows,
+                                                          uint32_t T, float scale) {
+    const uint32_t row = blockIdx.x * 16 + (threadIdx.x >> 4), l = threadIdx.x & 15;
+    if (row >= rows)
+        return;
+    float *x = S + (size_t)row * Ts;
+    float m = -INFINITY;
+    for (uint32_t j = l; j < T; j += 16)
+        m = __builtin_fmaxf(m, x[j] * scale);
+    m = __builtin_fmaxf(m, __shfl_xor(m, 8, 16));
+    m = __builtin_fmaxf(m, __shfl_xor(m, 4, 16));
+    m = __builtin_fmaxf(m, __shfl_xor(m, 2, 16));
+    m = __builtin_fmaxf(m, __shfl_xor(m, 1, 16));
+    float acc = 0.0f;
+    for (uint32_t j = l; j < T; j += 16) {
+        const float e = pk_expf(x[j] * scale - m);
+        x[j] = e;
+        acc += e;
+    }
+    const float inv = 1.0f / lanes16_sum(acc);
+    for (uint32_t j = l; j < T; j += 16)
+        x[j] = x[j] * inv;
+}
+
+constexpr int kPI = 32, kPD = 64, kPJ = 32;    /* queries, dimensions, keys a stage */
+
+__global__ __launch_bounds__(128) void att_pv_kernel(float *__restrict__ of, const float *__restrict__ S,
+                                                     uint32_t Ts, const float *__restrict__ vf, uint32_t T,
+                                                     uint32_t D, uint32_t dk) {
+    __shared__ float sP[kPI][kPJ + 1], sV[kPJ][kPD + 1];
+    const uint32_t d0 = blockIdx.x * kPD, i0 = blockIdx.y * kPI, h = blockIdx.z;
+    const int tid = threadIdx.x, ti = tid >> 4, td = tid & 15;
+    const float *Sh = S + (size_t)h * T * Ts;
+    const uint32_t col = h * dk + d0;
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+            acc[a][b] = 0.0f;
+    for (uint32_t j0 = 0; j0 < T; j0 += kPJ) {
+        for (int e = tid; e < kPI * kPJ; e += 128) {
+            const int r = e / kPJ, c = e % kPJ;
+            const uint32_t i = i0 + r, j = j0 + c;
+            sP[r][c] = i < T && j < T ? Sh[(size_t)i * Ts + j] : 0.0f;
+        }
+        for (int e = tid; e < kPJ * kPD; e += 128) {
+            const int r = e / kPD, c = e % kPD;
+            const uint32_t j = j0 + r;
+            sV[r][c] = j < T ? vf[(size_t)j * D + col + c] : 0.0f;
+        }
+        __syncthreads();
+        /* exactly the T keys: a padding term would turn a -0 sum into +0 */
+        const int jn = T - j0 < (uint32_t)kPJ ? (int)(T - j0) : kPJ;
+        for (int c = 0; c < jn; c++) {
+            float p[4], v[4];
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                p[a] = sP[ti + 8 * a][c];
+                v[a] = sV[c][td + 16 * a];
+            }
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++)
+                    acc[a][b] = __builtin_fmaf(v[b], p[a], acc[a][b]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const uint32_t i = i0 + ti + 8 * a;
+        if (i < T)
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                of[(size_t)i * D + col + td + 16 * b] = acc[a][b];
+    }
+}
+
+/* --------------------------------------------------------------- dwq --
+ *
+ * core/encoder.c:158-176 (glu_item, dw_item): h = GLU(u) (backend/ref/
+ * kernels.c:157-161), the depthwise convolution of K taps with its bias
+ * and SiLU (backend/ref/kernels.c:163-176, the taps past the ends skipped),
+ * and the blocks' quantize of each frame's 64 channels (whole blocks of 32
+ * or 64). One workgroup a group of 16 frames and 64 channels, which is one
+ * packed unit: h for the frames the taps reach goes through LDS, a lane
+ * takes a channel, and the unit is put together in LDS and leaves as 1 KB. */
+constexpr int kMaxTaps = 33;
+
+__device__ __forceinline__ int half_max_nonneg(int v, int lane) {
+    v = group_max_nonneg<16>(v);
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false));   /* row_bcast15: rows 1, 3 */
+    const int lo = __builtin_amdgcn_readlane(v, 31), hi = __builtin_amdgcn_readlane(v, 63);
+    return lane < 32 ? lo : hi;
+}
+
+template <int QB>
+__global__ __launch_bounds__(256) void dwq_kernel(int8_t *__restrict__ qp, float *__restrict__ d,
+                                                  const float *__restrict__ u, uint32_t T, uint32_t D,
+                                                  const float *__restrict__ w, const float *__restrict__ b,
+                                                  uint32_t K) {
+    __shared__ float hs[16 + kMaxTaps - 1][64];
+    __shared__ __attribute__((aligned(16))) int8_t unit[kUnitBytes];
+    const uint32_t g = blockIdx.x, G = gridDim.x, c0 = blockIdx.y * 64, t0 = 16 * g;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t half = K / 2;
+    const uint32_t rows = 16 + K - 1;
+    for (uint32_t e = tid; e < rows * 64; e += 256) {
+        const uint32_t r = e / 64, c = e % 64;
+        const int64_t s = (int64_t)t0 - half + r;
+        float hv = 0.0f;
+        if (s >= 0 && s < (int64_t)T) {
+            const float *us = u + (size_t)s * 2 * D + c0 + c;
+            hv = us[0] * pk_sigmoidf(us[D]);
+        }
+        hs[r][c] = hv;
+    }
+    __syncthreads();
+    const uint32_t c = c0 + lane;
+    const float bc = b[c];
+    const float *wc = w + (size_t)c * K;
+    for (int f = 0; f < 4; f++) {
+        const uint32_t r = 4 * wv + f, t = t0 + r;
+        float y = 0.0f;
+        if (t < T) {
+            float acc = 0.0f;
+            for (uint32_t j = 0; j < K; j++) {
+                const int64_t s = (int64_t)t + j - half;
+                if (s >= 0 && s < (int64_t)T)
+                    acc = __builtin_fmaf(wc[j], hs[r + j][lane], acc);
+            }
+            const float v = acc + bc;
+            y = v * pk_sigmoidf(v);
+        }
+        const uint32_t mb = (uint32_t)(QB == 64 ? wave_max_nonneg(mag_bits(y)) : half_max_nonneg(mag_bits(y), lane));
+        const bool zero = zero_bits(mb);
+        float dv = 0.0f, id = 0.0f;
+        if (!zero) {
+            const float amax = __uint_as_float(mb);
+            dv = amax / 127.0f;
+            id = 127.0f / amax;
+        }
+        unit[in_unit(lane, r)] = (int8_t)(zero ? 0 : q1(y, id));
+        if (t < T && lane % QB == 0)
+            d[(size_t)t * (D / QB) + c / QB] = dv;
+    }
+    __syncthreads();
+    if (tid < 64)
+        *(v4i *)(qp + ((size_t)(c0 / 64) * G + g) * kUnitBytes + 16 * tid) = *(const v4i *)(unit + 16 * tid);
+}
+
+/* ---------------------------------------------------------- launchers -- */
+
+int launch_normq(int8_t *qp, float *d, const float *x, uint32_t n, uint32_t T, const float *w, const float *b,
+                 float eps, uint32_t qb, hipStream_t s) {
+    if (T == 0)
+        return 0;
+    if (n % 64 || n > 4096 || !(qb == n || qb == 32 || qb == 64))
+        return -2;
+    const uint32_t grid = (T + 3) / 4;
+    const bool small = n <= 1024;
+#define PK_NQ(CH, QB) normq_kernel<CH, QB><<<grid, 256, 0, s>>>(qp, d, x, n, T, w, b, eps)
+    if (qb == n) {
+        if (small) PK_NQ(4, 0); else PK_NQ(16, 0);
+    } else if (qb == 32) {
+        if (small) PK_NQ(4, 32); else PK_NQ(16, 32);
+    } else {
+        if (small) PK_NQ(4, 64); else PK_NQ(16, 64);
+    }
+#undef PK_NQ
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b, float eps, hipStream_t s) {
+    if (T == 0)
+        return 0;
+    if (n % 64 || n > 4096)
+        return -2;
+    if (n <= 1024)
+        norm_kernel<4><<<(T + 3) / 4, 256, 0, s>>>(x, n, T, w, b, eps);
+    else
+        norm_kernel<16><<<(T + 3) / 4, 256, 0, s>>>(x, n, T, w, b, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+uint32_t att_score_stride(uint32_t T) { return (T + 3) & ~3u; }
+
+int launch_attention(float *of, float *S, const float *qf, const float *kf, const float *vf, const float *pf,
+                     const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s) {
+    if (T == 0)
+        return 0;
+    if (H == 0 || D % H || (D / H) % kPD)
+        return -2;
+    const uint32_t dk = D / H, Ts = att_score_stride(T), tiles = (T + kAT - 1) / kAT;
+    att_scores_kernel<<<dim3(tiles, tiles, H), 256, 0, s>>>(S, Ts, qf, kf, pf, bu, bv, T, D, dk);
+    const uint32_t rows = H * T;
+    const float scale = 1.0f / sqrtf((float)dk);
+    att_softmax_kernel<<<(rows + 15) / 16, 256, 0, s>>>(S, Ts, rows, T, scale);
+    att_pv_kernel<<<dim3(dk / kPD, (T + kPI - 1) / kPI, H), 128, 0, s>>>(of, S, Ts, vf, T, D, dk);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_dwq(int8_t *qp, float *d, const float *u, uint32_t T, uint32_t D, const float *w, const float *b,
+               uint32_t K, uint32_t qb, hipStream_t s) {
+    if (T == 0)
+        return 0;
+    if (D % 64 || K == 0 || K > (uint32_t)kMaxTaps || !(qb == 32 || qb == 64))
+        return -2;
+    const dim3 grid((T + 15) / 16, D / 64);
+    if (qb == 32)
+        dwq_kernel<32><<<grid, 256, 0, s>>>(qp, d, u, T, D, w, b, K);
+    else
+        dwq_kernel<64><<<grid, 256, 0, s>>>(qp, d, u, T, D, w, b, K);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace pkq8

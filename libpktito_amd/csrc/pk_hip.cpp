@@ -756,3 +756,241 @@ int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, c
 }
 
 }  // extern "C"
+
+/* ----------------------------------------- the device-resident layer --- */
+
+namespace {
+
+bool al16(const void *p) { return p && ((uintptr_t)p & 15) == 0; }
+
+bool blocks_ok(const pk_hip_act *a, bool whole) {
+    return ((a->qb == 32 || a->qb == 64) && a->n % a->qb == 0) || (whole && a->qb == a->n);
+}
+
+#define PK_LAUNCH(call, what)                                            \
+    do {                                                                 \
+        if ((call))                                                      \
+            return hip_fail(hipGetLastError(), what);                    \
+    } while (0)
+
+/* The layer's workspace, carved in 256-byte aligned pieces; with base NULL
+ * only the size. */
+struct LayerWs {
+    int8_t *act_qp, *hid_qp;
+    float *act_d, *hid_d, *u, *qf, *kf, *vf, *pf, *S, *of;
+};
+
+size_t layer_carve(LayerWs *w, char *base, const pk_hip_layer *L, uint32_t T, uint32_t qb) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        char *p = base ? base + off : nullptr;
+        off += (bytes + 255) & ~(size_t)255;
+        return p;
+    };
+    const size_t D = L->D, F = L->F, R = 2 * (size_t)T - 1, U = F > 2 * D ? F : 2 * D;
+    w->act_qp = (int8_t *)take(pkq8::packed_bytes(L->D, T));
+    w->act_d = (float *)take(T * (D / qb) * 4);
+    w->hid_qp = (int8_t *)take(pkq8::packed_bytes(L->F, T));
+    w->hid_d = (float *)take(T * (F / qb) * 4);
+    w->u = (float *)take(T * U * 4);
+    w->qf = (float *)take(T * D * 4);
+    w->kf = (float *)take(T * D * 4);
+    w->vf = (float *)take(T * D * 4);
+    w->pf = (float *)take(R * D * 4);
+    w->S = (float *)take((size_t)L->H * T * pkq8::att_score_stride(T) * 4);
+    w->of = (float *)take(T * D * 4);
+    return off;
+}
+
+bool mat_is(const pk_hip_q8 *m, uint32_t rows, uint32_t cols) { return m && m->rows == rows && m->cols == cols; }
+
+int layer_check(const pk_hip_layer *L, uint32_t qb) {
+    if (!L)
+        return fail(PK_HIP_EINVAL, "layer_dev: no layer");
+    const uint32_t D = L->D, F = L->F, H = L->H;
+    if (D == 0 || D % 64 || D > 4096 || F == 0 || F % 64 || F > 4096 || H == 0 || D % H || (D / H) % 64 ||
+        L->K == 0 || L->K > 33 || !(qb == 32 || qb == 64) || !(L->eps >= 0.0f))
+        return fail(PK_HIP_EINVAL, "layer_dev: D and F multiples of 64 up to 4096, heads of a multiple of 64, "
+                                   "1 to 33 taps, blocks of 32 or 64");
+    const float *v[] = { L->ff1_nw, L->ff1_nb, L->att_nw, L->att_nb, L->conv_nw, L->conv_nb, L->ff2_nw,
+                         L->ff2_nb, L->out_nw, L->out_nb, L->bias_u, L->bias_v, L->dw_b };
+    for (const float *p : v)
+        if (!al16(p))
+            return fail(PK_HIP_EINVAL, "layer_dev: a vector is NULL or not 16-byte aligned");
+    if (!L->dw)
+        return fail(PK_HIP_EINVAL, "layer_dev: dw is NULL");
+    if (!mat_is(L->ff1_up, F, D) || !mat_is(L->ff2_up, F, D) || !mat_is(L->ff1_down, D, F) ||
+        !mat_is(L->ff2_down, D, F) || !mat_is(L->q, D, D) || !mat_is(L->k, D, D) || !mat_is(L->v, D, D) ||
+        !mat_is(L->pos, D, D) || !mat_is(L->o, D, D) || !mat_is(L->pw1, 2 * D, D) || !mat_is(L->pw2, D, D))
+        return fail(PK_HIP_ENOTUP, "layer_dev: a matrix is missing or of the wrong shape");
+    return PK_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pk_hip_normq_dev(pk_hip_act *a, int8_t *qp, const float *x, const float *w, const float *b, float eps,
+                     void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!a)
+        return fail(PK_HIP_EINVAL, "normq_dev: act is NULL");
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!a->d || !al16(qp) || !al16(x) || !al16(w) || !al16(b) || a->n == 0 || a->n % 64 || a->n > 4096 ||
+        !blocks_ok(a, true))
+        return fail(PK_HIP_EINVAL, "normq_dev: n a multiple of 64 up to 4096 in blocks of the whole row, 32 or "
+                                   "64; d set, qp, x, w and b 16-byte aligned");
+    PK_LAUNCH(pkq8::launch_normq(qp, a->d, x, a->n, a->T, w, b, eps, a->qb, (hipStream_t)stream), "normq launch");
+    g_kernel = "normq";
+    return PK_HIP_OK;
+}
+
+int pk_hip_siluq_dev(pk_hip_act *a, int8_t *qp, const float *x, size_t xs, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!a)
+        return fail(PK_HIP_EINVAL, "siluq_dev: act is NULL");
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!a->d || !al16(qp) || !al16(x) || a->n == 0 || a->n % 32 || a->n > 4096 || !blocks_ok(a, true) ||
+        xs < a->n || xs % 4)
+        return fail(PK_HIP_EINVAL, "siluq_dev: n a multiple of 32 up to 4096 in blocks of the whole row, 32 or "
+                                   "64; d set, qp and x 16-byte aligned, xs >= n and a multiple of 4");
+    const char *name = "";
+    PK_LAUNCH(pkq8::launch_quantize_packed(nullptr, qp, a->d, x, xs, a->n, a->qb, a->T, (hipStream_t)stream,
+                                           &name, pkq8::kOpSilu),
+              "siluq launch");
+    g_kernel = name;
+    return PK_HIP_OK;
+}
+
+int pk_hip_dwq_dev(pk_hip_act *a, int8_t *qp, const float *u, const float *w, const float *b, uint32_t K,
+                   void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!a)
+        return fail(PK_HIP_EINVAL, "dwq_dev: act is NULL");
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!a->d || !al16(qp) || !u || !w || !b || a->n == 0 || a->n % 64 || !blocks_ok(a, false) || K == 0 ||
+        K > 33)
+        return fail(PK_HIP_EINVAL, "dwq_dev: n a multiple of 64 in blocks of 32 or 64, 1 to 33 taps; d, u, w, b "
+                                   "set and qp 16-byte aligned");
+    PK_LAUNCH(pkq8::launch_dwq(qp, a->d, u, a->T, a->n, w, b, K, a->qb, (hipStream_t)stream), "dwq launch");
+    g_kernel = "dwq";
+    return PK_HIP_OK;
+}
+
+int pk_hip_layernorm_dev(float *x, uint32_t T, uint32_t n, const float *w, const float *b, float eps,
+                         void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (T == 0)
+        return PK_HIP_OK;
+    if (!al16(x) || !al16(w) || !al16(b) || n == 0 || n % 64 || n > 4096)
+        return fail(PK_HIP_EINVAL, "layernorm_dev: n a multiple of 64 up to 4096; x, w, b 16-byte aligned");
+    PK_LAUNCH(pkq8::launch_norm(x, n, T, w, b, eps, (hipStream_t)stream), "layernorm launch");
+    g_kernel = "norm";
+    return PK_HIP_OK;
+}
+
+size_t pk_hip_attention_workspace(uint32_t T, uint32_t H) {
+    return (size_t)H * T * pkq8::att_score_stride(T) * sizeof(float);
+}
+
+int pk_hip_attention_dev(float *o, const float *q, const float *k, const float *v, const float *p,
+                         const float *bias_u, const float *bias_v, uint32_t T, uint32_t D, uint32_t H, void *ws,
+                         size_t ws_bytes, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (T == 0)
+        return PK_HIP_OK;
+    if (!o || !q || !k || !v || !p || !bias_u || !bias_v || !ws || H == 0 || D % H || (D / H) % 64)
+        return fail(PK_HIP_EINVAL, "attention_dev: heads of a multiple of 64 dimensions, every pointer set");
+    if (ws_bytes < pk_hip_attention_workspace(T, H))
+        return fail(PK_HIP_EINVAL, "attention_dev: workspace of %zu bytes, %zu needed", ws_bytes,
+                    pk_hip_attention_workspace(T, H));
+    PK_LAUNCH(pkq8::launch_attention(o, (float *)ws, q, k, v, p, bias_u, bias_v, T, D, H, (hipStream_t)stream),
+              "attention launch");
+    g_kernel = "attention";
+    return PK_HIP_OK;
+}
+
+size_t pk_hip_layer_workspace(const pk_hip_layer *L, uint32_t T, uint32_t qb) {
+    if (!L || T == 0 || !(qb == 32 || qb == 64))
+        return 0;
+    LayerWs w;
+    return layer_carve(&w, nullptr, L, T, qb);
+}
+
+int pk_hip_layer_dev(const pk_hip_layer *L, float *x, uint32_t T, const int8_t *ape_qp, const float *ape_d,
+                     uint32_t qb, void *ws, size_t ws_bytes, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if ((e = layer_check(L, qb)))
+        return e;
+    if (T == 0)
+        return PK_HIP_OK;
+    if (!al16(x) || !al16(ape_qp) || !ape_d || !al16(ws))
+        return fail(PK_HIP_EINVAL, "layer_dev: x, ape_qp and ws 16-byte aligned, ape_d set");
+    LayerWs w;
+    const size_t need = layer_carve(&w, (char *)ws, L, T, qb);
+    if (ws_bytes < need)
+        return fail(PK_HIP_EINVAL, "layer_dev: workspace of %zu bytes, %zu needed", ws_bytes, need);
+    hipStream_t s = (hipStream_t)stream;
+    const uint32_t D = L->D, F = L->F, R = 2 * T - 1;
+    pk_hip_act act = { nullptr, w.act_d, D, qb, T }, hid = { nullptr, w.hid_d, F, qb, T };
+    pk_hip_act ape = { nullptr, const_cast<float *>(ape_d), D, qb, R };
+    const char *name = "";
+    auto gemm = [&](float *out, size_t os, const pk_hip_q8 *m, const pk_hip_act *a, const int8_t *qp, int add) {
+        return launch_product(out, os, m, 0, m->rows, m->s, nullptr, a, add, 0, s, qp);
+    };
+    /* ff (core/encoder.c:321-327): x += down(siluq(up(normq(x)))) */
+    auto ff = [&](const float *nw, const float *nb, const pk_hip_q8 *up, const pk_hip_q8 *down) {
+        PK_LAUNCH(pkq8::launch_normq(w.act_qp, w.act_d, x, D, T, nw, nb, L->eps, qb, s), "layer normq launch");
+        int r = gemm(w.u, F, up, &act, w.act_qp, 0);
+        if (r)
+            return r;
+        PK_LAUNCH(pkq8::launch_quantize_packed(nullptr, w.hid_qp, w.hid_d, w.u, F, F, qb, T, s, &name,
+                                               pkq8::kOpSilu),
+                  "layer siluq launch");
+        return gemm(x, D, down, &hid, w.hid_qp, 1);
+    };
+    if ((e = ff(L->ff1_nw, L->ff1_nb, L->ff1_up, L->ff1_down)))
+        return e;
+    /* the attention (core/encoder.c:339-352) */
+    PK_LAUNCH(pkq8::launch_normq(w.act_qp, w.act_d, x, D, T, L->att_nw, L->att_nb, L->eps, qb, s),
+              "layer normq launch");
+    if ((e = gemm(w.qf, D, L->q, &act, w.act_qp, 0)) || (e = gemm(w.kf, D, L->k, &act, w.act_qp, 0)) ||
+        (e = gemm(w.vf, D, L->v, &act, w.act_qp, 0)) || (e = gemm(w.pf, D, L->pos, &ape, ape_qp, 0)))
+        return e;
+    PK_LAUNCH(pkq8::launch_attention(w.of, w.S, w.qf, w.kf, w.vf, w.pf, L->bias_u, L->bias_v, T, D, L->H, s),
+              "layer attention launch");
+    PK_LAUNCH(pkq8::launch_quantize_packed(nullptr, w.act_qp, w.act_d, w.of, D, D, qb, T, s, &name),
+              "layer quantize launch");
+    if ((e = gemm(x, D, L->o, &act, w.act_qp, 1)))
+        return e;
+    /* the convolution module (core/encoder.c:354-362) */
+    PK_LAUNCH(pkq8::launch_normq(w.act_qp, w.act_d, x, D, T, L->conv_nw, L->conv_nb, L->eps, qb, s),
+              "layer normq launch");
+    if ((e = gemm(w.u, 2 * D, L->pw1, &act, w.act_qp, 0)))
+        return e;
+    PK_LAUNCH(pkq8::launch_dwq(w.act_qp, w.act_d, w.u, T, D, L->dw, L->dw_b, L->K, qb, s), "layer dwq launch");
+    if ((e = gemm(x, D, L->pw2, &act, w.act_qp, 1)))
+        return e;
+    if ((e = ff(L->ff2_nw, L->ff2_nb, L->ff2_up, L->ff2_down)))
+        return e;
+    PK_LAUNCH(pkq8::launch_norm(x, D, T, L->out_nw, L->out_nb, L->eps, s), "layer norm launch");
+    g_kernel = "layer";
+    return PK_HIP_OK;
+}
+
+}  // extern "C"

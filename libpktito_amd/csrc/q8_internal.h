@@ -77,7 +77,7 @@ int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, 
 /* Quantize (n <= 4096; qb == n, 32 or 64) writing the packed copy qp, and
  * the row-major q too when q is not NULL. */
 int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
-                           uint32_t qb, uint32_t T, hipStream_t s, const char **name);
+                           uint32_t qb, uint32_t T, hipStream_t s, const char **name, int op = 0);
 
 /* The pipelined product's tilings: how many, and forcing one (-1: the
  * heuristic); returns the one forced before. */
@@ -87,6 +87,21 @@ int set_ring(int i);
 /* The packed quantize's kernel: 0 one wave a column, 1 one workgroup a
  * group, -1 by size; returns the one forced before. */
 int set_quant_kernel(int kind);
+
+/* The quantize's op on its inputs (launch_quantize_packed's op). */
+constexpr int kOpPlain = 0, kOpSilu = 1;
+
+/* The device-resident layer's float kernels (layer_kernels.hip): 0, -2 for
+ * shapes they do not take, -1 for a failed launch. */
+int launch_normq(int8_t *qp, float *d, const float *x, uint32_t n, uint32_t T, const float *w, const float *b,
+                 float eps, uint32_t qb, hipStream_t s);
+int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b, float eps, hipStream_t s);
+/* The attention's scores are H x T rows of att_score_stride(T) floats. */
+uint32_t att_score_stride(uint32_t T);
+int launch_attention(float *of, float *S, const float *qf, const float *kf, const float *vf, const float *pf,
+                     const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s);
+int launch_dwq(int8_t *qp, float *d, const float *u, uint32_t T, uint32_t D, const float *w, const float *b,
+               uint32_t K, uint32_t qb, hipStream_t s);
 
 /* One product; table->nseg == 1 for a plain call. */
 int launch_gemm(const GemmArgs &g, const SegTable &table, hipStream_t s, const char **name);

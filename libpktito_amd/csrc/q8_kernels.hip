@@ -11,6 +11,7 @@
  * (a block's scale can be subnormal) or relaxes division.
  */
 #include "q8_internal.h"
+#include "q8_device.h"
 
 #include <float.h>
 #include <stdio.h>
@@ -21,8 +22,6 @@
 
 namespace pkq8 {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
 /* ------------------------------------------------------------ quantize --
  *
  * backend/ref/kernels.c:24-58, per column t and block b of qb inputs:
@@ -30,13 +29,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
  *   otherwise d = amax / 127, id = 127 / amax, q = rint(x * id)
  * amax is a max, the same in any order. Both divisions are IEEE divisions
  * (hipcc's default correctly rounded fp32 divide), rint is v_rndne_f32. */
-
-__device__ __forceinline__ int q1(float v, float id) { return (int)__builtin_rintf(v * id); }
-
-__device__ __forceinline__ int pack4(float4 v, float id) {
-    return (q1(v.x, id) & 0xff) | (q1(v.y, id) & 0xff) << 8 | (q1(v.z, id) & 0xff) << 16 |
-           (q1(v.w, id) & 0xff) << 24;
-}
 
 __device__ __forceinline__ void absmax4(float4 v, float &amax, int &nan) {
     nan |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
@@ -50,14 +42,6 @@ __device__ __forceinline__ bool zero_block(float amax, int nan) {
     return nan || !__builtin_isfinite(amax) || amax < 0x1p-121f;
 }
 
-/* The same block rule on magnitude bits: m = the largest (bits & 0x7fffffff)
- * of the block. Non-negative floats order as their bit patterns do, NaN above
- * infinity above every finite value, so the block holds a NaN or an infinity
- * exactly when m >= 0x7f800000, and otherwise m is the bits of amax; 2^-121
- * is 0x03000000. */
-__device__ __forceinline__ bool zero_bits(uint32_t m) { return m >= 0x7f800000u || m < 0x03000000u; }
-
-__device__ __forceinline__ int mag_bits(float v) { return (int)(__float_as_uint(v) & 0x7fffffffu); }
 
 /* Output stores: non-temporal (the products never read their outputs back,
  * and a product's outputs all leave at its end: measured, the stores drain
@@ -71,18 +55,6 @@ __device__ __forceinline__ void store_out4(float *o, float4 v) {
 
 __device__ __forceinline__ void store_out1(float *o, float v) { __builtin_nontemporal_store(v, o); }
 
-/* The maximum over the wave of a non-negative int, in every lane: DPP within
- * rows of 16 lanes (quad swaps, half mirror, mirror), the row broadcasts
- * across rows, then lane 63's value. All 64 lanes must be active. */
-__device__ __forceinline__ int wave_max_nonneg(int v) {
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));    /* quad_perm 1,0,3,2 */
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));    /* quad_perm 2,3,0,1 */
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));   /* row_half_mirror */
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));   /* row_mirror */
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false));   /* row_bcast15: rows 1, 3 */
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false));   /* row_bcast31: rows 2, 3 */
-    return __builtin_amdgcn_readlane(v, 63);
-}
 
 /* A whole column is one block (qb == n, "per-row" quantization): one
  * workgroup of W waves a column, each thread up to CH chunks of 16 inputs,
@@ -221,71 +193,20 @@ __global__ __launch_bounds__(256) void quant_any_kernel(int8_t *__restrict__ q, 
     d[i] = dv;
 }
 
-/* max of a non-negative int over aligned groups of W lanes (W = 8 or 16), in
- * every lane of the group: DPP quad swaps, half mirror, and mirror for 16 */
-template <int W>
-__device__ __forceinline__ int group_max_nonneg(int v) {
-    static_assert(W == 8 || W == 16, "groups of 8 or 16 lanes");
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
-    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
-    if constexpr (W == 16)
-        v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
-    return v;
-}
-
-__device__ __forceinline__ int mag4(float4 f) {
-    return max(max(mag_bits(f.x), mag_bits(f.y)), max(mag_bits(f.z), mag_bits(f.w)));
-}
-
-/* The scales of a column of n <= 4096 inputs that one wave holds, each lane
- * CH float4 chunks of it (chunk c of lane l is float4 l + 64 c, zeros past
- * the column). QB == 0: the column is one block, reduced over the wave;
- * QB == 32 or 64: chunk c's block of QB inputs, reduced within the QB / 4
- * lanes holding it. All 64 lanes active. */
-template <int CH, int QB>
-struct WaveScales {
-    static constexpr int NB = QB ? CH : 1;
-    float dv[NB], id[NB];
-    bool zero[NB];
-
-    __device__ __forceinline__ void block(int b, uint32_t mb) {
-        zero[b] = zero_bits(mb);
-        dv[b] = 0.0f;
-        id[b] = 0.0f;
-        if (!zero[b]) {
-            const float amax = __uint_as_float(mb);
-            dv[b] = amax / 127.0f;
-            id[b] = 127.0f / amax;
-        }
-    }
-
-    __device__ __forceinline__ explicit WaveScales(const float4 (&v)[CH]) {
-        if constexpr (QB == 0) {
-            int m = 0;
-#pragma unroll
-            for (int c = 0; c < CH; c++)
-                m = max(m, mag4(v[c]));
-            block(0, (uint32_t)wave_max_nonneg(m));
-        } else {
-#pragma unroll
-            for (int c = 0; c < CH; c++)
-                block(c, (uint32_t)group_max_nonneg<QB / 4>(mag4(v[c])));
-        }
-    }
-};
-
-/* Where inputs k..k+3 of frame r of a 16-frame group sit in the group's
- * unit k / 64: at 16 (16 kq + r) + k % 16, kq = (k % 64) / 16. Unit u of
- * group g is unit u G + g of the packed copy of G groups. */
-__device__ __forceinline__ uint32_t in_unit(uint32_t k, uint32_t r) {
-    return (((k >> 4) & 3) * 16 + r) * 16 + (k & 15);
-}
-
 /* One wave a column of n <= 4096 inputs, four columns a workgroup (the
  * quantizes of up to about 7M inputs, where the kernel is one memory round
  * trip and wants its loads spread over the most CUs). */
-template <int CH, bool PACK, int QB>
+/* What a quantize does to its inputs first: nothing, or SiLU (the feed-
+ * forward's hidden activations, core/encoder.c:147-156). */
+template <int OP>
+__device__ __forceinline__ float4 quant_in(float4 v) {
+    if constexpr (OP == kOpSilu)
+        return make_float4(pk_silu(v.x), pk_silu(v.y), pk_silu(v.z), pk_silu(v.w));
+    else
+        return v;
+}
+
+template <int CH, bool PACK, int QB, int OP = kOpPlain>
 __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q, int8_t *__restrict__ qp,
                                                          float *__restrict__ d, const float *__restrict__ x,
                                                          size_t xs, uint32_t n, uint32_t T) {
@@ -299,7 +220,7 @@ __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q,
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
-        v[c] = i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[c] = i < n4 ? quant_in<OP>(xr[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     const WaveScales<CH, QB> sc(v);
     int *qr = (int *)(q + (size_t)t * n);
@@ -333,7 +254,7 @@ __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q,
  * product that reads the copy next finds it in the memory-side cache, and
  * a layer of ten minutes of audio took 2% longer with non-temporal stores.
  * Columns past T are written as zero rows of the group. */
-template <int CH, int QB>
+template <int CH, int QB, int OP = kOpPlain>
 __global__ __launch_bounds__(1024) void quant_group_kernel(int8_t *__restrict__ q, int8_t *__restrict__ qp,
                                                            float *__restrict__ d, const float *__restrict__ x,
                                                            size_t xs, uint32_t n, uint32_t T) {
@@ -347,7 +268,7 @@ __global__ __launch_bounds__(1024) void quant_group_kernel(int8_t *__restrict__ 
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
-        v[c] = live && i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[c] = live && i < n4 ? quant_in<OP>(xr[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     const WaveScales<CH, QB> sc(v);
     int *qr = (int *)(q + (size_t)t * n);
@@ -388,23 +309,20 @@ int set_quant_kernel(int kind) {
     return was;
 }
 
-int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
-                           uint32_t qb, uint32_t T, hipStream_t s, const char **name) {
-    if (T == 0)
-        return 0;
+template <int OP>
+static int launch_quantize_packed_op(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
+                                     uint32_t qb, uint32_t T, hipStream_t s, const char **name) {
     const uint32_t n4 = n / 4;
-    if (n4 > 1024 || !(qb == n || qb == 32 || qb == 64))
-        return -2;
     const bool small = n4 <= 256;
     const bool group = g_quant_kernel < 0 ? (uint64_t)T * n >= kGroupQuantInputs : g_quant_kernel == 1;
 #define PK_QP(CH, QB, NAME)                                                                       \
     do {                                                                                          \
         if (group) {                                                                              \
-            quant_group_kernel<CH, QB><<<(T + 15) / 16, 1024, 0, s>>>(q, qp, d, x, xs, n, T);    \
-            *name = "quant_group_packed" NAME;                                                    \
+            quant_group_kernel<CH, QB, OP><<<(T + 15) / 16, 1024, 0, s>>>(q, qp, d, x, xs, n, T);    \
+            *name = OP ? "quant_group_packed_silu" NAME : "quant_group_packed" NAME;                                                    \
         } else {                                                                                  \
-            quant_wave_kernel<CH, true, QB><<<(T + 3) / 4, 256, 0, s>>>(q, qp, d, x, xs, n, T);  \
-            *name = "quant_wave_packed" NAME;                                                     \
+            quant_wave_kernel<CH, true, QB, OP><<<(T + 3) / 4, 256, 0, s>>>(q, qp, d, x, xs, n, T);  \
+            *name = OP ? "quant_wave_packed_silu" NAME : "quant_wave_packed" NAME;                                                     \
         }                                                                                         \
     } while (0)
     if (qb == n) {
@@ -416,6 +334,18 @@ int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size
     }
 #undef PK_QP
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
+                           uint32_t qb, uint32_t T, hipStream_t s, const char **name, int op) {
+    if (T == 0)
+        return 0;
+    const uint32_t n4 = n / 4;
+    if (n4 > 1024 || !(qb == n || qb == 32 || qb == 64) || (op != kOpPlain && op != kOpSilu))
+        return -2;
+    if (op == kOpSilu)
+        return launch_quantize_packed_op<kOpSilu>(q, qp, d, x, xs, n, qb, T, s, name);
+    return launch_quantize_packed_op<kOpPlain>(q, qp, d, x, xs, n, qb, T, s, name);
 }
 
 int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb,

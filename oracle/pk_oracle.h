@@ -20,6 +20,20 @@
  *                  (16 columns an item)
  *   pko_rnd ...    tests/kcheck.c:40-60 (xorshift64*, frand, awkward)
  *
+ * and in pk_oracle_layer.c, the float kernels around the products and the
+ * encoder layer they make (the device-resident layer's definition):
+ *
+ *   pko_expf, pko_sigmoidf    core/vmath.h:126-151 (the reference's own
+ *                             exp polynomial, not libm's)
+ *   pko_gemm_f32              backend/ref/kernels.c:90-105
+ *   pko_layernorm             backend/ref/kernels.c:109-132 (16-lane sums)
+ *   pko_softmax, pko_silu,    backend/ref/kernels.c:134-176
+ *   pko_glu, pko_dwconv
+ *   pko_conformer_layer       core/encoder.c:108-128 (normq), 147-156
+ *                             (siluq_tile), 170-176 (dw_item), 280-327
+ *                             (att_item), 321-368 (ff, layer);
+ *                             core/passes.c:164-236 (the attention's panels)
+ *
  * How each is pinned, beyond restating the formula:
  *   - against the reference's own compiled ref backend (oracle/_ref, built
  *     from the reference's sources by oracle/Makefile) on seeded cases;
@@ -29,7 +43,15 @@
  *   - the epilogue against the d = 0, s < 0 case where fmaf(s, d, +0) is +0
  *     and a bare product -0, and against directed rounding modes;
  *   - the quantizer against its invariants (q in [-127, 127], zero block
- *     exactly when NaN, inf or amax < 2^-121, d = amax / 127 rounded once).
+ *     exactly when NaN, inf or amax < 2^-121, d = amax / 127 rounded once);
+ *   - the float kernels against the reference's compiled ref table and its
+ *     inline pk_expf / pk_sigmoidf (oracle/_ref) on seeded rows with NaNs,
+ *     infinities, ties and the clamp's ends, pko_expf also against exp in
+ *     double (within 1 ulp on [-87, 88]) and pko_layernorm against a
+ *     float64 layer norm; the layer is these kernels and the int8 path
+ *     composed in core/encoder.c's order, pinned through each of them and
+ *     through invariants of the whole (a frame's outputs depend on other
+ *     frames only through the attention and the convolution's K taps).
  * Every function here is pinned by at least one of these (tests/test_oracle.py).
  */
 #ifndef PK_ORACLE_H
@@ -71,6 +93,50 @@ void  pko_gemm_threads(pko_gemm_fn fn, int nthreads, float *out, size_t os, cons
                        const float *ws, const float *bias, uint32_t rows, const pko_act *a, int add);
 /* The quantizer over nthreads, 16 columns an item. */
 void  pko_quantize_threads(pko_quant_fn fn, int nthreads, pko_act *a, const float *x, size_t xs);
+
+/* ------------------------------------------ float kernels and a layer --- */
+
+float pko_expf(float x);
+float pko_sigmoidf(float x);
+void  pko_expf_n(float *y, const float *x, size_t n);       /* y[i] = pko_expf(x[i]) */
+void  pko_sigmoidf_n(float *y, const float *x, size_t n);
+void  pko_gemm_f32(float *out, size_t os, const float *w, uint32_t ld, uint32_t rows, uint32_t n,
+                   const float *x, size_t xs, uint32_t T, const float *bias, size_t bs, int relu);
+void  pko_layernorm(float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t n,
+                    const float *w, const float *b, float eps);
+void  pko_softmax(float *x, uint32_t n, float scale);
+void  pko_silu(float *x, size_t n);
+void  pko_glu(float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t n);
+void  pko_dwconv(float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t C,
+                 const float *w, const float *b, uint32_t K);
+
+/* A PK_Q8 matrix (core/model.h:39-43): panels, a scale a row. */
+typedef struct {
+    const int8_t *q;
+    const float  *s;
+    uint32_t      rows, cols;
+} pko_q8;
+
+/* One encoder layer's weights (core/model.h:45-53) and shapes: D = d_model,
+ * H heads of D / H, F = ff_dim, K the depthwise taps. */
+typedef struct {
+    uint32_t D, H, F, K;
+    float    eps;
+    const float *ff1_nw, *ff1_nb, *att_nw, *att_nb, *conv_nw, *conv_nb;
+    const float *ff2_nw, *ff2_nb, *out_nw, *out_nb;
+    pko_q8 ff1_up, ff1_down, ff2_up, ff2_down;
+    pko_q8 q, k, v, pos, o;
+    const float *bias_u, *bias_v;
+    pko_q8 pw1, pw2;
+    const float *dw, *dw_b;
+} pko_layer;
+
+/* One layer in place on x [T][D]: ape holds the positions' activations,
+ * 2T - 1 frames of D quantized in blocks of qb (core/encoder.c:467-469), the
+ * layer's blocks qb too. The products over nthreads. 0, or -1 for shapes
+ * the layer does not take, -2 when out of memory. */
+int   pko_conformer_layer(const pko_layer *L, float *x, uint32_t T, const pko_act *ape, uint32_t qb,
+                          int nthreads);
 
 /* kcheck's generator: xorshift64*, state kept by the caller. */
 uint32_t pko_rnd(uint64_t *s);

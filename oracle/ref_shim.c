@@ -10,6 +10,7 @@
  */
 #include "kernels.h"
 #include "pk_oracle.h"
+#include "vmath.h"
 
 #include <string.h>
 
@@ -65,4 +66,43 @@ void pkref_gemm_threads(int i, int nthreads, float *out, size_t os, const int8_t
 
 void pkref_quantize_threads(int i, int nthreads, pk_act *a, const float *x, size_t xs) {
     pko_quantize_threads((pko_quant_fn)tables[i]->quantize, nthreads, (pko_act *)a, x, xs);
+}
+
+/* The reference's float kernels and its inline exp and sigmoid
+ * (core/vmath.h:134-151), for pinning the oracle's restatements. */
+float pkref_expf(float x) { return pk_expf(x); }
+
+float pkref_sigmoidf(float x) { return pk_sigmoidf(x); }
+
+void pkref_expf_n(float *y, const float *x, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = pk_expf(x[i]);
+}
+
+void pkref_sigmoidf_n(float *y, const float *x, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = pk_sigmoidf(x[i]);
+}
+
+void pkref_gemm_f32(int i, float *out, size_t os, const float *w, uint32_t ld, uint32_t rows, uint32_t n,
+                    const float *x, size_t xs, uint32_t T, const float *bias, size_t bs, int relu) {
+    tables[i]->gemm_f32(out, os, w, ld, rows, n, x, xs, T, bias, bs, relu);
+}
+
+void pkref_layernorm(int i, float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t n,
+                     const float *w, const float *b, float eps) {
+    tables[i]->layernorm(out, os, x, xs, T, n, w, b, eps);
+}
+
+void pkref_softmax(int i, float *x, uint32_t n, float scale) { tables[i]->softmax(x, n, scale); }
+
+void pkref_silu(int i, float *x, size_t n) { tables[i]->silu(x, n); }
+
+void pkref_glu(int i, float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t n) {
+    tables[i]->glu(out, os, x, xs, T, n);
+}
+
+void pkref_dwconv(int i, float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t C,
+                  const float *w, const float *b, uint32_t K) {
+    tables[i]->dwconv(out, os, x, xs, T, C, w, b, K);
 }

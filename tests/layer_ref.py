@@ -1,0 +1,76 @@
+"""Shared by the layer tests: random layer weights in the oracle's dict
+form, the positions' activations, the attention composed from a backend's
+float kernels, and the packed activations' layout read back. Test
+infrastructure."""
+import numpy as np
+
+import oracle_lib as ol
+from libpktito_amd import synth
+
+
+def layer_weights(g, D, H, F, K, eps=1e-5):
+    """Random weights of one layer in the oracle's dict form (int8 uniform,
+    row scales small enough that the residual stream stays O(1))."""
+    w = {"D": D, "H": H, "F": F, "K": K, "eps": eps}
+    for n in ol.LAYER_NORMS:
+        w[n] = (1.0 + 0.1 * g.standard_normal(D)) if n.endswith("nw") else 0.1 * g.standard_normal(D)
+    shapes = {"ff1_up": (F, D), "ff1_down": (D, F), "ff2_up": (F, D), "ff2_down": (D, F), "q": (D, D),
+              "k": (D, D), "v": (D, D), "pos": (D, D), "o": (D, D), "pw1": (2 * D, D), "pw2": (D, D)}
+    for n, (rows, cols) in shapes.items():
+        w[n + "_rm"] = synth.weights(g, rows, cols)
+        w[n] = synth.pack_q8(w[n + "_rm"])
+        w[n + "_s"] = (g.uniform(0.5, 1.5, rows) / (127.0 * np.sqrt(cols))).astype(np.float32)
+    w["bias_u"] = 0.1 * g.standard_normal(D)
+    w["bias_v"] = 0.1 * g.standard_normal(D)
+    w["dw"] = 0.3 * g.standard_normal((D, K))
+    w["dw_b"] = 0.1 * g.standard_normal(D)
+    return {k: (v.astype(np.float32) if isinstance(v, np.ndarray) and v.dtype == np.float64 else v)
+            for k, v in w.items()}
+
+
+def positions(g, T, D, qb):
+    ape = g.standard_normal((2 * T - 1, D)).astype(np.float32)
+    q, d = ol.quantize(ape.reshape(-1), 2 * T - 1, D, qb, D)
+    return ape, q, d
+
+
+def attention(q, k, v, p, bias_u, bias_v, H, impl="oracle"):
+    """core/encoder.c:280-327 from a backend's pk_k_gemm_f32 and pk_k_softmax
+    (the oracle's, or the reference's with impl="ref"), with the operands laid
+    out here by numpy as that kernel's panels: o [T, D] from q, k, v [T, D]
+    and the positions' p [2T - 1, D]."""
+    T, D = q.shape
+    R, dk = 2 * T - 1, D // H
+    scale = np.float32(1.0) / np.sqrt(np.float32(dk))
+    o = np.zeros((T, D), np.float32)
+
+    def panels(m, rows):
+        # 16 rows a panel, k-major: W(d, j) at ((j / 16) dk + d) 16 + j % 16
+        pad = np.zeros(((rows + 15) // 16 * 16, dk), np.float32)
+        pad[:rows] = m
+        return pad.reshape(-1, 16, dk).transpose(0, 2, 1).reshape(-1)
+
+    for h in range(H):
+        hs = slice(h * dk, (h + 1) * dk)
+        qu = (q[:, hs] + bias_u[hs]).astype(np.float32)
+        qv = (q[:, hs] + bias_v[hs]).astype(np.float32)
+        sc = ol.gemm_f32(panels(k[:, hs], T), dk, (T + 15) // 16 * 16, dk, qu, T, impl=impl)[:, :T]
+        bd = ol.gemm_f32(panels(p[:, hs], R), dk, (R + 15) // 16 * 16, dk, qv, T, impl=impl)
+        s = np.empty((T, T), np.float32)
+        for i in range(T):
+            s[i] = sc[i] + bd[i, T - 1 - i:2 * T - 1 - i]
+        s = ol.softmax(s, scale, impl=impl)
+        # values as panels of 16 dimensions, key-major
+        vp = np.ascontiguousarray(v[:, hs].T).reshape(dk // 16, 16, T).transpose(0, 2, 1).reshape(-1)
+        o[:, hs] = ol.gemm_f32(vp, T, dk, T, s, T, impl=impl)
+    return o
+
+
+def unpack_packed(qp, n, T):
+    """Packed activations (16-frame groups, units of 16 x 64 in MFMA order,
+    stage-major) back to row-major [T, n]."""
+    G = (T + 15) // 16
+    ku = len(qp) // (G * 1024)
+    u = qp.reshape(ku, G, 4, 16, 16)            # [unit][group][kq][row][16 bytes]
+    full = u.transpose(1, 3, 0, 2, 4).reshape(G * 16, ku * 64)
+    return full[:T, :n]

@@ -24,6 +24,39 @@ _GEMM = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p, cty
 _oracle = None
 _ref = None
 
+_P, _Z, _U, _F, _I = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_float, ctypes.c_int
+
+
+def _float_sigs(l, pre, first):
+    """argtypes of the float kernels, under prefix pre, with the extra leading
+    arguments `first` (the backend index for the reference's)."""
+    getattr(l, pre + "expf_n").argtypes = [_P, _P, _Z]
+    getattr(l, pre + "sigmoidf_n").argtypes = [_P, _P, _Z]
+    getattr(l, pre + "gemm_f32").argtypes = first + [_P, _Z, _P, _U, _U, _U, _P, _Z, _U, _P, _Z, _I]
+    getattr(l, pre + "layernorm").argtypes = first + [_P, _Z, _P, _Z, _U, _U, _P, _P, _F]
+    getattr(l, pre + "softmax").argtypes = first + [_P, _U, _F]
+    getattr(l, pre + "silu").argtypes = first + [_P, _Z]
+    getattr(l, pre + "glu").argtypes = first + [_P, _Z, _P, _Z, _U, _U]
+    getattr(l, pre + "dwconv").argtypes = first + [_P, _Z, _P, _Z, _U, _U, _P, _P, _U]
+
+
+class Q8(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("s", ctypes.c_void_p), ("rows", ctypes.c_uint32),
+                ("cols", ctypes.c_uint32)]
+
+
+LAYER_NORMS = ("ff1_nw", "ff1_nb", "att_nw", "att_nb", "conv_nw", "conv_nb", "ff2_nw", "ff2_nb", "out_nw",
+               "out_nb")
+LAYER_MATS = ("ff1_up", "ff1_down", "ff2_up", "ff2_down", "q", "k", "v", "pos", "o", "pw1", "pw2")
+
+
+class Layer(ctypes.Structure):
+    _fields_ = ([("D", ctypes.c_uint32), ("H", ctypes.c_uint32), ("F", ctypes.c_uint32), ("K", ctypes.c_uint32),
+                 ("eps", ctypes.c_float)] + [(n, ctypes.c_void_p) for n in LAYER_NORMS] +
+                [(n, Q8) for n in ("ff1_up", "ff1_down", "ff2_up", "ff2_down", "q", "k", "v", "pos", "o")] +
+                [("bias_u", ctypes.c_void_p), ("bias_v", ctypes.c_void_p), ("pw1", Q8), ("pw2", Q8),
+                 ("dw", ctypes.c_void_p), ("dw_b", ctypes.c_void_p)])
+
 
 def oracle():
     """liboracle.so, built with the oracle's Makefile if missing (gcc only)."""
@@ -42,6 +75,9 @@ def oracle():
         l.pko_gemm_threads.argtypes = [ctypes.c_void_p, ctypes.c_int] + _GEMM
         l.pko_quantize_threads.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(Act),
                                            ctypes.c_void_p, ctypes.c_size_t]
+        _float_sigs(l, "pko_", [])
+        l.pko_conformer_layer.argtypes = [ctypes.POINTER(Layer), ctypes.c_void_p, ctypes.c_uint32,
+                                          ctypes.POINTER(Act), ctypes.c_uint32, ctypes.c_int]
         _oracle = l
     return _oracle
 
@@ -58,6 +94,7 @@ def ref():
         l.pkref_gemm_threads.argtypes = [ctypes.c_int, ctypes.c_int] + _GEMM
         l.pkref_quantize_threads.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(Act),
                                              ctypes.c_void_p, ctypes.c_size_t]
+        _float_sigs(l, "pkref_", [ctypes.c_int])
         _ref = l
     return _ref
 
@@ -114,3 +151,104 @@ def definition(w, ws, bias, rows, q, d, n, qb, T):
     a = Act(_p(q), _p(d), n, qb, T)
     oracle().pko_definition(_p(out), rows, _p(w), _p(ws), _p(bias), rows, ctypes.byref(a))
     return out
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def expf(x, impl="oracle"):
+    """core/vmath.h's pk_expf over an array, by the oracle or the reference."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    (oracle().pko_expf_n if impl == "oracle" else ref().pkref_expf_n)(_p(y), _p(x), x.size)
+    return y
+
+
+def sigmoidf(x, impl="oracle"):
+    x = _f32(x)
+    y = np.empty_like(x)
+    (oracle().pko_sigmoidf_n if impl == "oracle" else ref().pkref_sigmoidf_n)(_p(y), _p(x), x.size)
+    return y
+
+
+def _float_call(name, impl, *args):
+    if impl == "oracle":
+        return getattr(oracle(), "pko_" + name)(*args)
+    return getattr(ref(), "pkref_" + name)(ref_index(impl), *args)
+
+
+def layernorm(x, w, b, eps, impl="oracle"):
+    """pk_k_layernorm over the rows of x [T, n] into a new array."""
+    x = _f32(x)
+    T, n = x.shape
+    out = np.empty_like(x)
+    _float_call("layernorm", impl, _p(out), n, _p(x), n, T, n, _p(_f32(w)), _p(_f32(b)), eps)
+    return out
+
+
+def softmax(x, scale, impl="oracle"):
+    """pk_k_softmax of each row of x [R, n], into a new array."""
+    x = _f32(x).copy()
+    for r in range(x.shape[0]):
+        _float_call("softmax", impl, x[r].ctypes.data, x.shape[1], scale)
+    return x
+
+
+def silu(x, impl="oracle"):
+    x = _f32(x).copy()
+    _float_call("silu", impl, _p(x), x.size)
+    return x
+
+
+def glu(x, impl="oracle"):
+    """pk_k_glu of x [T, 2n] into [T, n]."""
+    x = _f32(x)
+    T, n2 = x.shape
+    out = np.empty((T, n2 // 2), np.float32)
+    _float_call("glu", impl, _p(out), n2 // 2, _p(x), n2, T, n2 // 2)
+    return out
+
+
+def dwconv(x, w, b, impl="oracle"):
+    """pk_k_dwconv of x [T, C] with taps w [C, K] and bias b [C]."""
+    x = _f32(x)
+    T, C = x.shape
+    w = _f32(w)
+    out = np.empty_like(x)
+    _float_call("dwconv", impl, _p(out), C, _p(x), C, T, C, _p(w), _p(_f32(b)), w.shape[1])
+    return out
+
+
+def gemm_f32(w_panels, ld, rows, n, x, T, bias=None, bs=0, relu=0, impl="oracle"):
+    """pk_k_gemm_f32 with its panel layout; out [T, rows]."""
+    x = _f32(x)
+    out = np.empty((T, rows), np.float32)
+    _float_call("gemm_f32", impl, _p(out), rows, _p(_f32(w_panels)), ld, rows, n, _p(x), x.shape[1] if x.ndim > 1
+                else n, T, _p(_f32(bias)) if bias is not None else None, bs, relu)
+    return out
+
+
+def conformer_layer(weights, x, T, ape_q, ape_d, qb, threads=8):
+    """pko_conformer_layer on a copy of x [T, D]; weights is a dict of numpy
+    arrays (LAYER_NORMS, bias_u, bias_v, dw, dw_b, and for each of LAYER_MATS
+    the PK_Q8 panels `name` and row scales `name_s`) with the shapes D, H, F,
+    K and eps. Returns the new x."""
+    L = Layer(D=weights["D"], H=weights["H"], F=weights["F"], K=weights["K"], eps=weights["eps"])
+    keep = []
+    for n in LAYER_NORMS + ("bias_u", "bias_v", "dw", "dw_b"):
+        a = _f32(weights[n])
+        keep.append(a)
+        setattr(L, n, a.ctypes.data)
+    for n in LAYER_MATS:
+        q = np.ascontiguousarray(weights[n], dtype=np.int8)
+        s = _f32(weights[n + "_s"])
+        keep += [q, s]
+        setattr(L, n, Q8(q.ctypes.data, s.ctypes.data, s.size, q.size // s.size))
+    y = _f32(x).copy()
+    D = weights["D"]
+    a = Act(_p(ape_q), _p(ape_d), D, qb, 2 * T - 1)
+    rc = oracle().pko_conformer_layer(ctypes.byref(L), _p(y), T, ctypes.byref(a), qb, threads)
+    if rc:
+        raise ValueError(f"pko_conformer_layer: {rc}")
+    return y

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as ol
+from layer_ref import unpack_packed
 from libpktito_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -154,16 +155,6 @@ def test_interior_panels_device(hip, torch):
     want_nob = old.copy()
     ol.gemm_q8(want_nob, os_, w, ws, None, rows, q, d, K, K, M, 1, r0=r0)
     assert np.array_equal(bits(ot.cpu().numpy()), bits(want_nob))
-
-
-def unpack_packed(qp, n, T):
-    """Packed activations (16-frame groups, units of 16 x 64 in MFMA order,
-    stage-major) back to row-major [T, n]."""
-    G = (T + 15) // 16
-    ku = len(qp) // (G * 1024)
-    u = qp.reshape(ku, G, 4, 16, 16)            # [unit][group][kq][row][16 bytes]
-    full = u.transpose(1, 3, 0, 2, 4).reshape(G * 16, ku * 64)
-    return full[:T, :n]
 
 
 @pytest.mark.parametrize("M,K,N", [(750, 1024, 4096), (1499, 1024, 1024), (300, 4096, 1024), (16, 1024, 4096),

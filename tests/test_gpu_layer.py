@@ -1,0 +1,184 @@
+"""The device-resident encoder layer on the GPU against the oracle, bit for
+bit (NaNs compared as NaN, the one thing the contract leaves to the
+hardware): each fused producer (normq, siluq, dwq) and the layer norm on
+rows with zeros, constants, NaNs and infinities; the attention at tile edges
+and at the model's heads; and whole layers, at small shapes and at the
+model's (d_model 1024, 8 heads, ff 4096, 9 taps), in blocks of 32 and 64."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from layer_ref import attention, layer_weights, positions, unpack_packed
+from libpktito_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return np.where(np.isnan(a), np.float32(np.nan), a).view(np.uint32)
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    assert torch.cuda.is_available()
+    return torch
+
+
+def rows_with_edges(g, T, n, scale=2.0):
+    """N(0, scale) + 0.5 with, when there are enough rows, a row of zeros, a
+    NaN, an infinity, a constant row and a row of subnormals."""
+    x = (g.standard_normal((T, n)) * scale + 0.5).astype(np.float32)
+    if T >= 6:
+        x[1] = 0.0
+        x[2, n // 3] = np.nan
+        x[3, 1] = np.inf
+        x[4] = 7.0
+        x[5] = np.float32(1e-40) * np.sign(x[5])
+    return x
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.device("cuda"))
+
+
+def packed_buffers(hip, torch, n, T, qb):
+    qp = torch.full((hip.packed_bytes(n, T),), -5, dtype=torch.int8, device="cuda")
+    d = torch.full((T * (n // qb),), 7.0, dtype=torch.float32, device="cuda")
+    return qp, d
+
+
+def check_packed(qp, d, q, dd, n, T):
+    assert np.array_equal(unpack_packed(qp.cpu().numpy(), n, T), q.reshape(T, n))
+    assert np.array_equal(bits(d.cpu().numpy()), bits(dd))
+
+
+@pytest.mark.parametrize("T,n,qb", [(1, 64, 64), (5, 1024, 32), (97, 1024, 64), (750, 1024, 32), (33, 4096, 4096),
+                                    (17, 256, 256), (40, 1024, 1024), (23, 4096, 64)])
+def test_normq(hip, torch, T, n, qb):
+    g = synth.rng(T + n + qb)
+    x = rows_with_edges(g, T, n)
+    w = (1 + 0.3 * g.standard_normal(n)).astype(np.float32)
+    b = (0.2 * g.standard_normal(n)).astype(np.float32)
+    q, d = ol.quantize(ol.layernorm(x, w, b, 1e-5).reshape(-1), T, n, qb, n)
+    qp, dt = packed_buffers(hip, torch, n, T, qb)
+    say("normq", T, n, qb)
+    hip.normq_dev(qp, dt, dev(torch, x), n, qb, T, dev(torch, w), dev(torch, b), 1e-5)
+    torch.cuda.synchronize()
+    check_packed(qp, dt, q, d, n, T)
+
+
+@pytest.mark.parametrize("T,n", [(1, 64), (7, 1024), (750, 1024), (19, 4096)])
+def test_layernorm(hip, torch, T, n):
+    g = synth.rng(T * n)
+    x = rows_with_edges(g, T, n, 3.0)
+    w = (1 + 0.3 * g.standard_normal(n)).astype(np.float32)
+    b = (0.2 * g.standard_normal(n)).astype(np.float32)
+    want = ol.layernorm(x, w, b, 1e-5)
+    xt = dev(torch, x)
+    say("layernorm", T, n)
+    hip.layernorm_dev(xt, T, n, dev(torch, w), dev(torch, b), 1e-5)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(xt.cpu().numpy()), bits(want))
+
+
+@pytest.mark.parametrize("T,n,qb", [(1, 32, 32), (9, 4096, 32), (750, 4096, 64), (100, 4096, 4096), (2049, 4096, 32)])
+def test_siluq(hip, torch, T, n, qb):
+    """SiLU then the quantize, both kernels of the packed quantize (the
+    largest case takes the one-workgroup-a-group kernel)."""
+    g = synth.rng(T + 3 * n + qb)
+    x = rows_with_edges(g, T, n, 4.0)
+    if T >= 8:
+        x[6, :] = np.float32(-90.0)            # past the exp clamp: SiLU of -90 is -0 * ...
+        x[7, ::2] = np.float32(88.5)
+    q, d = ol.quantize(ol.silu(x).reshape(-1), T, n, qb, n)
+    qp, dt = packed_buffers(hip, torch, n, T, qb)
+    say("siluq", T, n, qb)
+    hip.siluq_dev(qp, dt, dev(torch, x), n, qb, T, n)
+    torch.cuda.synchronize()
+    say("kernel", hip.last_kernel())
+    check_packed(qp, dt, q, d, n, T)
+
+
+@pytest.mark.parametrize("T,D,K,qb", [(1, 64, 9, 32), (2, 128, 9, 64), (9, 128, 9, 32), (17, 1024, 9, 32),
+                                      (100, 256, 31, 64), (750, 1024, 9, 64), (40, 128, 4, 32), (5, 64, 1, 64)])
+def test_dwq(hip, torch, T, D, K, qb):
+    """GLU, the depthwise convolution with its bias and SiLU, and the blocks'
+    quantize, against the oracle's glu, dwconv and quantize."""
+    g = synth.rng(T + D + K + qb)
+    u = (g.standard_normal((T, 2 * D)) * 2).astype(np.float32)
+    if T >= 3:
+        u[1, 3] = np.inf
+        u[2, D + 5] = -np.inf
+    w = (0.4 * g.standard_normal((D, K))).astype(np.float32)
+    b = (0.1 * g.standard_normal(D)).astype(np.float32)
+    h = ol.dwconv(ol.glu(u), w, b)
+    q, d = ol.quantize(h.reshape(-1), T, D, qb, D)
+    qp, dt = packed_buffers(hip, torch, D, T, qb)
+    say("dwq", T, D, K, qb)
+    hip.dwq_dev(qp, dt, dev(torch, u), D, qb, T, dev(torch, w), dev(torch, b), K)
+    torch.cuda.synchronize()
+    check_packed(qp, dt, q, d, D, T)
+
+
+@pytest.mark.parametrize("T,D,H", [(1, 128, 2), (2, 128, 2), (17, 128, 2), (64, 128, 2), (65, 256, 2),
+                                   (130, 128, 2), (100, 1024, 8)])
+def test_attention(hip, torch, T, D, H):
+    """The attention's scores (with the positions' diagonals), softmax and
+    weighted values against pk_k_gemm_f32 and pk_k_softmax composed on the
+    CPU with the reference's panel layouts."""
+    g = synth.rng(T * 7 + D)
+    q, k, v = (g.standard_normal((3, T, D)) * 1.5).astype(np.float32)
+    p = g.standard_normal((2 * T - 1, D)).astype(np.float32)
+    bu, bv = (0.3 * g.standard_normal((2, D))).astype(np.float32)
+    want = attention(q, k, v, p, bu, bv, H)
+    o = torch.full((T, D), 9.0, dtype=torch.float32, device="cuda")
+    ws = torch.empty((hip.attention_workspace(T, H),), dtype=torch.uint8, device="cuda")
+    say("attention", T, D, H)
+    hip.attention_dev(o, dev(torch, q), dev(torch, k), dev(torch, v), dev(torch, p), dev(torch, bu), dev(torch, bv),
+                      T, D, H, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(o.cpu().numpy()), bits(want))
+
+
+def run_layer(hip, torch, D, H, F, K, T, qb, seed, threads=16):
+    g = synth.rng(seed)
+    w = layer_weights(g, D=D, H=H, F=F, K=K)
+    x = g.standard_normal((T, D)).astype(np.float32)
+    ape, ape_q, ape_d = positions(g, T, D, qb)
+    R = 2 * T - 1
+    lay = hip.DeviceLayer(w, torch)
+    try:
+        ape_qp = torch.zeros((hip.packed_bytes(D, R),), dtype=torch.int8, device="cuda")
+        ape_dt = torch.empty((R * (D // qb),), dtype=torch.float32, device="cuda")
+        hip.quantize_packed_dev(None, ape_qp, ape_dt, dev(torch, ape), D, R, D, qb=qb)
+        ws = torch.empty((lay.workspace(T, qb),), dtype=torch.uint8, device="cuda")
+        xt = dev(torch, x)
+        say("layer", D, H, F, K, T, qb)
+        lay.run(xt, T, ape_qp, ape_dt, qb, ws)
+        torch.cuda.synchronize()
+        got = xt.cpu().numpy()
+        assert np.array_equal(unpack_packed(ape_qp.cpu().numpy(), D, R), ape_q.reshape(R, D))
+    finally:
+        lay.release()
+    want = ol.conformer_layer(w, x, T, ape_q, ape_d, qb, threads=threads)
+    assert np.all(np.isfinite(want))
+    assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("T,qb", [(1, 32), (2, 64), (37, 32), (100, 64)])
+def test_layer_small(hip, torch, T, qb):
+    run_layer(hip, torch, 128, 2, 256, 9, T, qb, seed=T * 3 + qb)
+
+
+@pytest.mark.parametrize("T,qb", [(64, 32), (150, 64)])
+def test_layer_model_shapes(hip, torch, T, qb):
+    run_layer(hip, torch, 1024, 8, 4096, 9, T, qb, seed=T + qb)
