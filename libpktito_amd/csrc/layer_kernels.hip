@@ -143,20 +143,31 @@ __global__ __launch_bounds__(256) void norm_kernel(float *__restrict__ x, uint32
  *               + chain_d fmaf(p_{T-1-i+j}[d], q_i[d] + v[d])
  * each chain over d = 0 .. dk-1 in order from +0 (pk_k_gemm_f32), the two
  * added once; softmax over the T keys (pk_k_softmax: the scale, the max,
- * pk_expf, the 16-lane sum, one division); then
+ * pk_expf, the 16-lane sum, one division, each e times 1 / sum); then
  *   o(i, d) = chain_j fmaf(v_j[d], P(i, j))  over j = 0 .. T-1 in order.
  * The reference lays K, P and V out as panels for its CPU kernel; the bits
  * depend only on each output's chain, so the products' row-major outputs
- * are read as they are.
+ * are read as they are. These are VALU kernels: an MFMA's sum of products
+ * rounds differently from a chain of FMAs.
  *
- * Three kernels: the scores of 64 x 64 (query, key) tiles, each thread a
- * 4 x 4 of them (queries ti + 16a, keys tj + 16b) with the head's
- * dimensions staged through LDS 32 at a time (queries with each bias,
- * keys, and the 127 position rows the tile's diagonals reach); the
- * softmax of each row in 16 lanes; and the weighted sum of the values,
- * 32 queries x 64 dimensions a workgroup, keys staged 32 at a time. */
-constexpr int kAT = 64;     /* queries and keys a score tile */
-constexpr int kADC = 32;    /* dimensions a stage */
+ * Three kernels:
+ *   scores   64 x 64 (query, key) tiles, each thread a 4 x 4 of them
+ *            (queries ti + 16a, keys tj + 16b) and both chains of each; the
+ *            head's dimensions staged 32 at a time through LDS (queries
+ *            with each bias, keys, and the 127 position rows the tile's
+ *            diagonals reach), read as float4 and prefetched a stage ahead;
+ *   softmax  16 lanes a row: writes e and the row's 1 / sum;
+ *   PV       32 queries x 32 dimensions a workgroup of 128, each thread 4
+ *            consecutive queries x 2 dimensions (8 chains: the work is
+ *            T^2 dk FMAs in only T dk chains, so the grid needs more,
+ *            thinner threads than a product); keys 32 at a time through
+ *            LDS with P = e * (1 / sum) formed as it is staged (the
+ *            reference's x[i] * inv, one rounding) and kept key-major for
+ *            one 16-byte read of a thread's 4 queries.
+ * Measured at T = 750, 8 heads of 128 (MI355X): 51, 14 and 43 us. */
+constexpr int kAT = 64;         /* queries and keys a score tile */
+constexpr int kADC = 32;        /* dimensions a stage */
+constexpr int kASD = kADC + 4;  /* an LDS row: 16-byte aligned, 4 banks apart */
 
 __global__ __launch_bounds__(256) void att_scores_kernel(float *__restrict__ S, uint32_t Ts,
                                                          const float *__restrict__ qf,
@@ -165,7 +176,8 @@ __global__ __launch_bounds__(256) void att_scores_kernel(float *__restrict__ S, 
                                                          const float *__restrict__ bu,
                                                          const float *__restrict__ bv, uint32_t T, uint32_t D,
                                                          uint32_t dk) {
-    __shared__ float squ[kAT][kADC + 1], sqv[kAT][kADC + 1], sk[kAT][kADC + 1], sp[2 * kAT - 1][kADC + 1];
+    __shared__ __attribute__((aligned(16))) float squ[kAT][kASD], sqv[kAT][kASD], sk[kAT][kASD],
+        sp[2 * kAT][kASD];
     const uint32_t j0 = blockIdx.x * kAT, i0 = blockIdx.y * kAT, h = blockIdx.z;
     const int tid = threadIdx.x, ti = tid >> 4, tj = tid & 15;
     const uint32_t R = 2 * T - 1;
@@ -177,43 +189,73 @@ __global__ __launch_bounds__(256) void att_scores_kernel(float *__restrict__ S, 
 #pragma unroll
         for (int b = 0; b < 4; b++)
             sc[a][b] = bd[a][b] = 0.0f;
-    for (uint32_t d0 = 0; d0 < dk; d0 += kADC) {
+    /* a stage in float4s: queries and keys 64 x 8 (2 a thread), positions
+     * 128 x 8 (4 a thread, the last row zeros) */
+    float4 rq[2], rk[2], rp[4];
+    auto load = [&](uint32_t d0) {
         const uint32_t col = h * dk + d0;
-        for (int e = tid; e < kAT * kADC; e += 256) {
-            const int r = e / kADC, c = e % kADC;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int e = tid + 256 * k, r = e / 8, c4 = e % 8;
             const uint32_t i = i0 + r, j = j0 + r;
-            const float q = i < T ? qf[(size_t)i * D + col + c] : 0.0f;
-            squ[r][c] = q + bu[col + c];
-            sqv[r][c] = q + bv[col + c];
-            sk[r][c] = j < T ? kf[(size_t)j * D + col + c] : 0.0f;
+            rq[k] = i < T ? *(const float4 *)(qf + (size_t)i * D + col + 4 * c4) : make_float4(0, 0, 0, 0);
+            rk[k] = j < T ? *(const float4 *)(kf + (size_t)j * D + col + 4 * c4) : make_float4(0, 0, 0, 0);
         }
-        for (int e = tid; e < (2 * kAT - 1) * kADC; e += 256) {
-            const int r = e / kADC, c = e % kADC;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = tid + 256 * k, r = e / 8, c4 = e % 8;
             const int64_t m = m0 + r;
-            sp[r][c] = m >= 0 && m < (int64_t)R ? pf[(size_t)m * D + col + c] : 0.0f;
+            rp[k] = r < 2 * kAT - 1 && m >= 0 && m < (int64_t)R
+                        ? *(const float4 *)(pf + (size_t)m * D + col + 4 * c4)
+                        : make_float4(0, 0, 0, 0);
         }
+    };
+    auto store = [&](uint32_t d0) {
+        const uint32_t col = h * dk + d0;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int e = tid + 256 * k, r = e / 8, c4 = e % 8;
+            const float4 u4 = *(const float4 *)(bu + col + 4 * c4), v4 = *(const float4 *)(bv + col + 4 * c4);
+            const float4 q = rq[k];
+            *(float4 *)&squ[r][4 * c4] = make_float4(q.x + u4.x, q.y + u4.y, q.z + u4.z, q.w + u4.w);
+            *(float4 *)&sqv[r][4 * c4] = make_float4(q.x + v4.x, q.y + v4.y, q.z + v4.z, q.w + v4.w);
+            *(float4 *)&sk[r][4 * c4] = rk[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = tid + 256 * k, r = e / 8, c4 = e % 8;
+            *(float4 *)&sp[r][4 * c4] = rp[k];
+        }
+    };
+    load(0);
+    for (uint32_t d0 = 0; d0 < dk; d0 += kADC) {
+        store(d0);
         __syncthreads();
-#pragma unroll 4
-        for (int c = 0; c < kADC; c++) {
-            float qu[4], qv[4], kk[4], pp[7];
+        if (d0 + kADC < dk)
+            load(d0 + kADC);
+#pragma unroll
+        for (int c = 0; c < kADC; c += 4) {
+            float4 qu[4], qv[4], kk[4], pp[7];
 #pragma unroll
             for (int a = 0; a < 4; a++) {
-                qu[a] = squ[ti + 16 * a][c];
-                qv[a] = sqv[ti + 16 * a][c];
-                kk[a] = sk[tj + 16 * a][c];
+                qu[a] = *(const float4 *)&squ[ti + 16 * a][c];
+                qv[a] = *(const float4 *)&sqv[ti + 16 * a][c];
+                kk[a] = *(const float4 *)&sk[tj + 16 * a][c];
             }
             /* query ti + 16a against key tj + 16b reads local position row
              * 63 - ti + tj + 16 (b - a) */
 #pragma unroll
             for (int e = 0; e < 7; e++)
-                pp[e] = sp[kAT - 1 - ti + tj + 16 * (e - 3)][c];
-#pragma unroll
-            for (int a = 0; a < 4; a++)
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    sc[a][b] = __builtin_fmaf(kk[b], qu[a], sc[a][b]);
-                    bd[a][b] = __builtin_fmaf(pp[b - a + 3], qv[a], bd[a][b]);
-                }
+                pp[e] = *(const float4 *)&sp[kAT - 1 - ti + tj + 16 * (e - 3)][c];
+            /* the four dimensions in order, every chain one FMA each */
+#define PK_ATT_DIM(F)                                                              \
+    _Pragma("unroll") for (int a = 0; a < 4; a++)                                \
+        _Pragma("unroll") for (int b = 0; b < 4; b++) {                          \
+            sc[a][b] = __builtin_fmaf(kk[b].F, qu[a].F, sc[a][b]);               \
+            bd[a][b] = __builtin_fmaf(pp[b - a + 3].F, qv[a].F, bd[a][b]);       \
+        }
+            PK_ATT_DIM(x) PK_ATT_DIM(y) PK_ATT_DIM(z) PK_ATT_DIM(w)
+#undef PK_ATT_DIM
         }
         __syncthreads();
     }
@@ -227,15 +269,17 @@ __global__ __launch_bounds__(256) void att_scores_kernel(float *__restrict__ S, 
         }
 }
 
-/* backend/ref/kernels.c:134-147 on rows of T scores, 16 lanes a row:
- * lane l takes keys l, l + 16, ... in order. */
-__global__ __launch_bounds__(256) void att_softmax_kernel(float *__restrict__ S, uint32_t Ts, uint32_t rows,
-                                                          uint32_t T, float scale) {
+/* backend/ref/kernels.c:134-147 on rows of T scores, 16 lanes a row
+ * (lane l takes keys l, l + 16, ... in order): each score becomes e, and
+ * the row's 1 / sum goes to inv; the multiply is PV's. */
+__global__ __launch_bounds__(256) void att_softmax_kernel(float *__restrict__ S, float *__restrict__ inv,
+                                                          uint32_t Ts, uint32_t rows, uint32_t T, float scale) {
     const uint32_t row = blockIdx.x * 16 + (threadIdx.x >> 4), l = threadIdx.x & 15;
     if (row >= rows)
         return;
     float *x = S + (size_t)row * Ts;
     float m = -INFINITY;
+#pragma unroll 8
     for (uint32_t j = l; j < T; j += 16)
         m = __builtin_fmaxf(m, x[j] * scale);
     m = __builtin_fmaxf(m, __shfl_xor(m, 8, 16));
@@ -243,68 +287,107 @@ __global__ __launch_bounds__(256) void att_softmax_kernel(float *__restrict__ S,
     m = __builtin_fmaxf(m, __shfl_xor(m, 2, 16));
     m = __builtin_fmaxf(m, __shfl_xor(m, 1, 16));
     float acc = 0.0f;
+#pragma unroll 8
     for (uint32_t j = l; j < T; j += 16) {
         const float e = pk_expf(x[j] * scale - m);
         x[j] = e;
         acc += e;
     }
-    const float inv = 1.0f / lanes16_sum(acc);
-    for (uint32_t j = l; j < T; j += 16)
-        x[j] = x[j] * inv;
+    const float r = 1.0f / lanes16_sum(acc);
+    if (l == 0)
+        inv[row] = r;
 }
 
-constexpr int kPI = 32, kPD = 64, kPJ = 32;    /* queries, dimensions, keys a stage */
+constexpr int kPI = 32, kPD = 32, kPJ = 32;    /* queries, dimensions, keys a stage of PV */
 
 __global__ __launch_bounds__(128) void att_pv_kernel(float *__restrict__ of, const float *__restrict__ S,
-                                                     uint32_t Ts, const float *__restrict__ vf, uint32_t T,
-                                                     uint32_t D, uint32_t dk) {
-    __shared__ float sP[kPI][kPJ + 1], sV[kPJ][kPD + 1];
+                                                     const float *__restrict__ inv, uint32_t Ts,
+                                                     const float *__restrict__ vf, uint32_t T, uint32_t D,
+                                                     uint32_t dk) {
+    constexpr int SPS = kPI + 4, SVS = kPD + 4;
+    constexpr int NP = kPI * kPJ / 128, NV = kPJ * kPD / 128;
+    __shared__ __attribute__((aligned(16))) float sPt[2][kPJ][SPS], sV[2][kPJ][SVS];
     const uint32_t d0 = blockIdx.x * kPD, i0 = blockIdx.y * kPI, h = blockIdx.z;
-    const int tid = threadIdx.x, ti = tid >> 4, td = tid & 15;
+    const int tid = threadIdx.x, tq = tid >> 4, td = tid & 15;    /* queries 4 tq .. +3, dims 2 td, +1 */
     const float *Sh = S + (size_t)h * T * Ts;
     const uint32_t col = h * dk + d0;
-    float acc[4][4];
+    float acc[4][2];
 #pragma unroll
     for (int a = 0; a < 4; a++)
+        acc[a][0] = acc[a][1] = 0.0f;
+    /* the rows a thread stages stay the same: their 1 / sum */
+    float rinv[NP], rp[NP], rv[NV];
 #pragma unroll
-        for (int b = 0; b < 4; b++)
-            acc[a][b] = 0.0f;
-    for (uint32_t j0 = 0; j0 < T; j0 += kPJ) {
-        for (int e = tid; e < kPI * kPJ; e += 128) {
-            const int r = e / kPJ, c = e % kPJ;
+    for (int k = 0; k < NP; k++) {
+        const uint32_t i = i0 + (tid + 128 * k) / kPJ;
+        rinv[k] = i < T ? inv[(size_t)h * T + i] : 0.0f;
+    }
+    auto load = [&](uint32_t j0) {
+#pragma unroll
+        for (int k = 0; k < NP; k++) {
+            const int e = tid + 128 * k, r = e / kPJ, c = e % kPJ;
             const uint32_t i = i0 + r, j = j0 + c;
-            sP[r][c] = i < T && j < T ? Sh[(size_t)i * Ts + j] : 0.0f;
+            rp[k] = i < T && j < T ? Sh[(size_t)i * Ts + j] : 0.0f;
         }
-        for (int e = tid; e < kPJ * kPD; e += 128) {
-            const int r = e / kPD, c = e % kPD;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int e = tid + 128 * k, r = e / kPD, c = e % kPD;
             const uint32_t j = j0 + r;
-            sV[r][c] = j < T ? vf[(size_t)j * D + col + c] : 0.0f;
+            rv[k] = j < T ? vf[(size_t)j * D + col + c] : 0.0f;
         }
-        __syncthreads();
-        /* exactly the T keys: a padding term would turn a -0 sum into +0 */
-        const int jn = T - j0 < (uint32_t)kPJ ? (int)(T - j0) : kPJ;
-        for (int c = 0; c < jn; c++) {
-            float p[4], v[4];
+    };
+    auto store = [&](int buf) {
 #pragma unroll
-            for (int a = 0; a < 4; a++) {
-                p[a] = sP[ti + 8 * a][c];
-                v[a] = sV[c][td + 16 * a];
-            }
-#pragma unroll
-            for (int a = 0; a < 4; a++)
-#pragma unroll
-                for (int b = 0; b < 4; b++)
-                    acc[a][b] = __builtin_fmaf(v[b], p[a], acc[a][b]);
+        for (int k = 0; k < NP; k++) {
+            const int e = tid + 128 * k;
+            sPt[buf][e % kPJ][e / kPJ] = rp[k] * rinv[k];
         }
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int e = tid + 128 * k;
+            sV[buf][e / kPD][e % kPD] = rv[k];
+        }
+    };
+    auto step = [&](int buf, int c) {
+        const float4 p = *(const float4 *)&sPt[buf][c][4 * tq];
+        const float2 v = *(const float2 *)&sV[buf][c][2 * td];
+        acc[0][0] = __builtin_fmaf(v.x, p.x, acc[0][0]);
+        acc[0][1] = __builtin_fmaf(v.y, p.x, acc[0][1]);
+        acc[1][0] = __builtin_fmaf(v.x, p.y, acc[1][0]);
+        acc[1][1] = __builtin_fmaf(v.y, p.y, acc[1][1]);
+        acc[2][0] = __builtin_fmaf(v.x, p.z, acc[2][0]);
+        acc[2][1] = __builtin_fmaf(v.y, p.z, acc[2][1]);
+        acc[3][0] = __builtin_fmaf(v.x, p.w, acc[3][0]);
+        acc[3][1] = __builtin_fmaf(v.y, p.w, acc[3][1]);
+    };
+    load(0);
+    store(0);
+    __syncthreads();
+    int buf = 0;
+    for (uint32_t j0 = 0; j0 < T; j0 += kPJ) {
+        const bool more = j0 + kPJ < T;
+        if (more)
+            load(j0 + kPJ);
+        if (T - j0 >= (uint32_t)kPJ) {
+#pragma unroll
+            for (int c = 0; c < kPJ; c++)
+                step(buf, c);
+        } else {
+            /* exactly the T keys: a padding term would turn a -0 sum into +0 */
+            const int jn = (int)(T - j0);
+            for (int c = 0; c < jn; c++)
+                step(buf, c);
+        }
+        if (more)
+            store(buf ^ 1);
         __syncthreads();
+        buf ^= 1;
     }
 #pragma unroll
     for (int a = 0; a < 4; a++) {
-        const uint32_t i = i0 + ti + 8 * a;
+        const uint32_t i = i0 + 4 * tq + a;
         if (i < T)
-#pragma unroll
-            for (int b = 0; b < 4; b++)
-                of[(size_t)i * D + col + td + 16 * b] = acc[a][b];
+            *(float2 *)(of + (size_t)i * D + col + 2 * td) = make_float2(acc[a][0], acc[a][1]);
     }
 }
 
@@ -417,18 +500,24 @@ int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b
 
 uint32_t att_score_stride(uint32_t T) { return (T + 3) & ~3u; }
 
-int launch_attention(float *of, float *S, const float *qf, const float *kf, const float *vf, const float *pf,
+size_t att_workspace_floats(uint32_t T, uint32_t H) {
+    /* the scores, then each row's 1 / sum (16-byte aligned: the stride is
+     * a multiple of 4 floats) */
+    return (size_t)H * T * att_score_stride(T) + (size_t)H * T;
+}
+
+int launch_attention(float *of, float *ws, const float *qf, const float *kf, const float *vf, const float *pf,
                      const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s) {
     if (T == 0)
         return 0;
-    if (H == 0 || D % H || (D / H) % kPD)
+    if (H == 0 || D % H || (D / H) % 64)
         return -2;
-    const uint32_t dk = D / H, Ts = att_score_stride(T), tiles = (T + kAT - 1) / kAT;
+    const uint32_t dk = D / H, Ts = att_score_stride(T), tiles = (T + kAT - 1) / kAT, rows = H * T;
+    float *S = ws, *inv = ws + (size_t)rows * Ts;
     att_scores_kernel<<<dim3(tiles, tiles, H), 256, 0, s>>>(S, Ts, qf, kf, pf, bu, bv, T, D, dk);
-    const uint32_t rows = H * T;
     const float scale = 1.0f / sqrtf((float)dk);
-    att_softmax_kernel<<<(rows + 15) / 16, 256, 0, s>>>(S, Ts, rows, T, scale);
-    att_pv_kernel<<<dim3(dk / kPD, (T + kPI - 1) / kPI, H), 128, 0, s>>>(of, S, Ts, vf, T, D, dk);
+    att_softmax_kernel<<<(rows + 15) / 16, 256, 0, s>>>(S, inv, Ts, rows, T, scale);
+    att_pv_kernel<<<dim3(dk / kPD, (T + kPI - 1) / kPI, H), 128, 0, s>>>(of, S, inv, Ts, vf, T, D, dk);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

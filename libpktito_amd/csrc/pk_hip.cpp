@@ -797,7 +797,7 @@ size_t layer_carve(LayerWs *w, char *base, const pk_hip_layer *L, uint32_t T, ui
     w->kf = (float *)take(T * D * 4);
     w->vf = (float *)take(T * D * 4);
     w->pf = (float *)take(R * D * 4);
-    w->S = (float *)take((size_t)L->H * T * pkq8::att_score_stride(T) * 4);
+    w->S = (float *)take(pkq8::att_workspace_floats(T, L->H) * 4);
     w->of = (float *)take(T * D * 4);
     return off;
 }
@@ -901,7 +901,7 @@ int pk_hip_layernorm_dev(float *x, uint32_t T, uint32_t n, const float *w, const
 }
 
 size_t pk_hip_attention_workspace(uint32_t T, uint32_t H) {
-    return (size_t)H * T * pkq8::att_score_stride(T) * sizeof(float);
+    return pkq8::att_workspace_floats(T, H) * sizeof(float);
 }
 
 int pk_hip_attention_dev(float *o, const float *q, const float *k, const float *v, const float *p,

@@ -96,9 +96,11 @@ constexpr int kOpPlain = 0, kOpSilu = 1;
 int launch_normq(int8_t *qp, float *d, const float *x, uint32_t n, uint32_t T, const float *w, const float *b,
                  float eps, uint32_t qb, hipStream_t s);
 int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b, float eps, hipStream_t s);
-/* The attention's scores are H x T rows of att_score_stride(T) floats. */
+/* The attention's workspace: H x T rows of att_score_stride(T) scores and
+ * H x T row sums' inverses, att_workspace_floats(T, H) floats. */
 uint32_t att_score_stride(uint32_t T);
-int launch_attention(float *of, float *S, const float *qf, const float *kf, const float *vf, const float *pf,
+size_t att_workspace_floats(uint32_t T, uint32_t H);
+int launch_attention(float *of, float *ws, const float *qf, const float *kf, const float *vf, const float *pf,
                      const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s);
 int launch_dwq(int8_t *qp, float *d, const float *u, uint32_t T, uint32_t D, const float *w, const float *b,
                uint32_t K, uint32_t qb, hipStream_t s);
