@@ -18,11 +18,16 @@ graph and replayed; K replays are timed with events on the stream they run
 on.
 
 Printed: one JSON line. `value` is TOPS (2 M K N over the step's time). The
-`extra` object adds the long-form layer (M = 7500) and a ragged batch of 8
-segments in grouped launches, the 24-layer chained encoder sweep in ms per
-audio-minute, and the skinny (M <= 16) shapes against HBM. `cpu_baseline`
-times the reference's own backends (compiled from its sources into
-oracle/_ref) on the host's cores, on the same inputs.
+`extra` object adds the same layer in the encoder's blocks of 32 and 64, the
+device-resident layer (the whole of core/encoder.c's layer in HBM: layer
+norms, SiLU and depthwise producers fused with their quantizes, the
+attention's float part and the eleven products, one pk_hip_layer_dev call)
+beside the same layer on the host's cores from the reference's own kernels,
+the long-form layer (M = 7500) and a ragged batch of 8 segments in grouped
+launches, the 24-layer chained encoder sweep in ms per audio-minute, and the
+skinny (M <= 16) shapes against HBM. `cpu_baseline` times the reference's own
+backends (compiled from its sources into oracle/_ref) on the host's cores,
+on the same inputs.
 """
 import argparse
 import ctypes
@@ -59,6 +64,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=8.0)
     p.add_argument("--profile-kernel", default=None,
                    help="only launch the named product's kernel 50 times (for rocprofv3 --pmc runs)")
+    p.add_argument("--profile-layer", type=int, default=0, metavar="QB",
+                   help="only replay the device-resident layer at M=750 in blocks of QB (for rocprofv3)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy 256 MiB three times (the known-size kernel that scales "
                         "rocprofv3's FETCH_SIZE / WRITE_SIZE)")
@@ -392,6 +399,59 @@ def cpu_baseline(prods_host, seconds):
     return results
 
 
+def device_layer(pk, torch, M, qb, reps=20, warmup=3):
+    """The device-resident encoder layer (core/encoder.c:321-368: its eleven
+    int8 products, the fused producers and the attention's float part) at M
+    frames in blocks of qb, one pk_hip_layer_dev call captured in a HIP graph
+    and replayed on the same x. Returns (us a layer, the weights and host
+    inputs for a CPU leg)."""
+    from libpktito_amd import synth
+    g = synth.rng(77 + qb)
+    w = synth.layer_weights(g, D=1024, H=8, F=4096, K=9)
+    x = g.standard_normal((M, 1024)).astype(np.float32)
+    ape = g.standard_normal((2 * M - 1, 1024)).astype(np.float32)
+    lay = pk.DeviceLayer(w, torch)
+    R = 2 * M - 1
+    ape_qp = torch.zeros((pk.packed_bytes(1024, R),), dtype=torch.int8, device="cuda")
+    ape_d = torch.empty((R * (1024 // qb),), dtype=torch.float32, device="cuda")
+    pk.quantize_packed_dev(None, ape_qp, ape_d, torch.from_numpy(ape).cuda(), 1024, R, 1024, qb=qb)
+    ws = torch.empty((lay.workspace(M, qb),), dtype=torch.uint8, device="cuda")
+    xt = torch.from_numpy(x).cuda()
+    gph = graph_of(torch, lambda: lay.run(xt, M, ape_qp, ape_d, qb, ws))
+    ms = time_graph(torch, gph, reps, warmup)
+    lay.release()
+    del gph
+    return ms * 1e3, (w, x, ape)
+
+
+def cpu_layer(w, x, ape, M, qb, seconds):
+    """The same layer on this host's cores from the reference's fastest
+    usable backend's own kernels (oracle/_ref), composed in core/encoder.c's
+    order and dealt over every core in the reference's items (the oracle's
+    composition, pinned to give the oracle's bits with them)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+    cores = min(os.cpu_count() or 1, 64)
+    impl, kind = "oracle", "port"
+    if ol.ref() is not None:
+        for bid in ("avx512-vnni", "avx2-vnni"):
+            i = ol.ref_index(bid)
+            if i >= 0 and ol.ref().pkref_usable(i):
+                impl, kind = bid, "reference"
+                break
+    R = 2 * M - 1
+    ape_q, ape_d = ol.quantize(ape.reshape(-1), R, 1024, qb, 1024)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        ol.conformer_layer(w, x, M, ape_q, ape_d, qb, threads=cores, impl=impl)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return dict(ms_per_layer=round(el / reps * 1e3, 2), layers=reps, seconds=round(el, 1), cores=cores,
+                kind=kind, backend=impl)
+
+
 def recorded_traffic(kernel, M, K, N):
     """HBM bytes a launch of this kernel on this shape, as the rocprofv3
     FETCH_SIZE / WRITE_SIZE passes summarized under profiles/ measured them
@@ -443,6 +503,11 @@ def main():
     torch.cuda.set_device(0)
 
     M = 750
+    if args.profile_layer:
+        us, _ = device_layer(pk, torch, M, args.profile_layer, reps=args.steps, warmup=args.warmup)
+        print(json.dumps({"profiled": "device_layer", "M": M, "qb": args.profile_layer, "us_per_layer": round(us, 1),
+                          "replays": args.steps}))
+        return
     prods = make_layer(pk, torch, M, seed=1)
     if args.profile_kernel:
         # the named product's kernel alone, 50 times: what the rocprofv3
@@ -517,6 +582,21 @@ def main():
         log(f"layer qb={qb}: {bms:.4f} ms")
         del gb
     extra["layer_M750_blocked"] = blocked
+
+    # the device-resident layer (the whole of core/encoder.c's layer in HBM:
+    # fused layer norm, SiLU and depthwise producers, the attention's float
+    # products, the eleven products), in the encoder's blocks
+    dlayer = {}
+    host_layer = None
+    for qb in (32, 64):
+        us, host = device_layer(pk, torch, M, qb)
+        dlayer[f"qb{qb}"] = dict(us_per_layer=round(us, 1), encoder_ms_per_audio_minute_24_layers=round(us * 24e-3, 2),
+                                 int8_product_tops=round(ops / (us * 1e-6) / 1e12, 1))
+        log(f"device layer qb={qb}: {us:.1f} us")
+        if qb == 32:
+            host_layer = host
+        torch.cuda.empty_cache()
+    extra["device_layer_M750"] = dlayer
 
     if not args.quick:
         # the long-form layer, M = 7500 (one segment of ten minutes)
@@ -671,6 +751,9 @@ def main():
         if not args.no_cpu:
             cpu = cpu_baseline(host_inputs, args.cpu_seconds)
             log("cpu baseline done")
+            w, x, ape = host_layer
+            extra["device_layer_M750"]["cpu_qb32"] = cpu_layer(w, x, ape, M, 32, args.cpu_seconds)
+            log("cpu layer done")
 
     line = {
         "metric": "int8 GEMM TOPS (% of MFMA peak); encoder-GEMM ms per audio-minute, 1 GPU",

@@ -130,3 +130,31 @@ class Counter:
         v = np.where(cls == 3, np.float32(-scale * 30.0), v)
         v = np.where(cls == 4, np.float32(scale * 0.5), v)
         return v.astype(np.float32)
+
+
+LAYER_VECTORS = ("ff1_nw", "ff1_nb", "att_nw", "att_nb", "conv_nw", "conv_nb", "ff2_nw", "ff2_nb", "out_nw",
+                 "out_nb")
+
+
+def layer_weights(g, D, H, F, K, eps=1e-5):
+    """Seeded random weights of one encoder layer (core/model.h:45-53) as a
+    dict of numpy arrays: the norms' weights and biases, for each matrix its
+    row-major int8 (`name_rm`), PK_Q8 bytes (`name`) and row scales
+    (`name_s`, small enough that the residual stream stays O(1)), the
+    attention's biases and the depthwise taps, and the shapes D, H, F, K,
+    eps."""
+    w = {"D": D, "H": H, "F": F, "K": K, "eps": eps}
+    for n in LAYER_VECTORS:
+        w[n] = (1.0 + 0.1 * g.standard_normal(D)) if n.endswith("nw") else 0.1 * g.standard_normal(D)
+    shapes = {"ff1_up": (F, D), "ff1_down": (D, F), "ff2_up": (F, D), "ff2_down": (D, F), "q": (D, D),
+              "k": (D, D), "v": (D, D), "pos": (D, D), "o": (D, D), "pw1": (2 * D, D), "pw2": (D, D)}
+    for n, (rows, cols) in shapes.items():
+        w[n + "_rm"] = weights(g, rows, cols)
+        w[n] = pack_q8(w[n + "_rm"])
+        w[n + "_s"] = (g.uniform(0.5, 1.5, rows) / (127.0 * np.sqrt(cols))).astype(np.float32)
+    w["bias_u"] = 0.1 * g.standard_normal(D)
+    w["bias_v"] = 0.1 * g.standard_normal(D)
+    w["dw"] = 0.3 * g.standard_normal((D, K))
+    w["dw_b"] = 0.1 * g.standard_normal(D)
+    return {k: (v.astype(np.float32) if isinstance(v, np.ndarray) and v.dtype == np.float64 else v)
+            for k, v in w.items()}

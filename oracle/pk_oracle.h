@@ -131,12 +131,36 @@ typedef struct {
     const float *dw, *dw_b;
 } pko_layer;
 
+/* A kernel table of the calls the layer makes (backend/kernels.h:242-278's
+ * entries), for composing the layer from the oracle's kernels or from a
+ * backend of the reference's (oracle/ref_shim.c fills one). */
+typedef struct {
+    void (*quantize)(pko_act *a, const float *x, size_t xs);
+    void (*gemm_q8)(float *out, size_t os, const int8_t *w, const float *ws, const float *bias, uint32_t rows,
+                    const pko_act *a, int add);
+    void (*gemm_f32)(float *out, size_t os, const float *w, uint32_t ld, uint32_t rows, uint32_t n,
+                     const float *x, size_t xs, uint32_t T, const float *bias, size_t bs, int relu);
+    void (*layernorm)(float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t n,
+                      const float *w, const float *b, float eps);
+    void (*softmax)(float *x, uint32_t n, float scale);
+    void (*silu)(float *x, size_t n);
+    void (*glu)(float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t n);
+    void (*dwconv)(float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t C,
+                   const float *w, const float *b, uint32_t K);
+} pko_kernels;
+
+extern const pko_kernels pko_kernels_oracle;
+
 /* One layer in place on x [T][D]: ape holds the positions' activations,
  * 2T - 1 frames of D quantized in blocks of qb (core/encoder.c:467-469), the
- * layer's blocks qb too. The products over nthreads. 0, or -1 for shapes
- * the layer does not take, -2 when out of memory. */
+ * layer's blocks qb too. Every pass over nthreads, dealt in the reference's
+ * items (16 frames, a head's 16 queries, 64 channels, 64-row slices). 0, or
+ * -1 for shapes the layer does not take, -2 when out of memory. The _with
+ * form takes the kernels from a table. */
 int   pko_conformer_layer(const pko_layer *L, float *x, uint32_t T, const pko_act *ape, uint32_t qb,
                           int nthreads);
+int   pko_conformer_layer_with(const pko_kernels *k, const pko_layer *L, float *x, uint32_t T,
+                               const pko_act *ape, uint32_t qb, int nthreads);
 
 /* kcheck's generator: xorshift64*, state kept by the caller. */
 uint32_t pko_rnd(uint64_t *s);

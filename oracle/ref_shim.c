@@ -106,3 +106,18 @@ void pkref_dwconv(int i, float *out, size_t os, const float *x, size_t xs, uint3
                   const float *w, const float *b, uint32_t K) {
     tables[i]->dwconv(out, os, x, xs, T, C, w, b, K);
 }
+
+/* Backend i's kernels as the oracle's table, for composing the layer from
+ * the reference's own kernels (pk_act and pko_act share one layout). */
+void pkref_kernels(int i, pko_kernels *k) {
+    const pk_kernels *t = tables[i];
+    k->quantize = (void (*)(pko_act *, const float *, size_t))t->quantize;
+    k->gemm_q8 = (void (*)(float *, size_t, const int8_t *, const float *, const float *, uint32_t,
+                           const pko_act *, int))t->gemm_q8;
+    k->gemm_f32 = t->gemm_f32;
+    k->layernorm = t->layernorm;
+    k->softmax = t->softmax;
+    k->silu = t->silu;
+    k->glu = t->glu;
+    k->dwconv = t->dwconv;
+}

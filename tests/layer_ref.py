@@ -6,26 +6,7 @@ import numpy as np
 
 import oracle_lib as ol
 from libpktito_amd import synth
-
-
-def layer_weights(g, D, H, F, K, eps=1e-5):
-    """Random weights of one layer in the oracle's dict form (int8 uniform,
-    row scales small enough that the residual stream stays O(1))."""
-    w = {"D": D, "H": H, "F": F, "K": K, "eps": eps}
-    for n in ol.LAYER_NORMS:
-        w[n] = (1.0 + 0.1 * g.standard_normal(D)) if n.endswith("nw") else 0.1 * g.standard_normal(D)
-    shapes = {"ff1_up": (F, D), "ff1_down": (D, F), "ff2_up": (F, D), "ff2_down": (D, F), "q": (D, D),
-              "k": (D, D), "v": (D, D), "pos": (D, D), "o": (D, D), "pw1": (2 * D, D), "pw2": (D, D)}
-    for n, (rows, cols) in shapes.items():
-        w[n + "_rm"] = synth.weights(g, rows, cols)
-        w[n] = synth.pack_q8(w[n + "_rm"])
-        w[n + "_s"] = (g.uniform(0.5, 1.5, rows) / (127.0 * np.sqrt(cols))).astype(np.float32)
-    w["bias_u"] = 0.1 * g.standard_normal(D)
-    w["bias_v"] = 0.1 * g.standard_normal(D)
-    w["dw"] = 0.3 * g.standard_normal((D, K))
-    w["dw_b"] = 0.1 * g.standard_normal(D)
-    return {k: (v.astype(np.float32) if isinstance(v, np.ndarray) and v.dtype == np.float64 else v)
-            for k, v in w.items()}
+from libpktito_amd.synth import layer_weights  # noqa: F401  (the tests' import point)
 
 
 def positions(g, T, D, qb):

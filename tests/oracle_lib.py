@@ -40,6 +40,12 @@ def _float_sigs(l, pre, first):
     getattr(l, pre + "dwconv").argtypes = first + [_P, _Z, _P, _Z, _U, _U, _P, _P, _U]
 
 
+class Kernels(ctypes.Structure):
+    """pko_kernels: the calls a layer makes, as function pointers."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("quantize", "gemm_q8", "gemm_f32", "layernorm", "softmax", "silu",
+                                               "glu", "dwconv")]
+
+
 class Q8(ctypes.Structure):
     _fields_ = [("q", ctypes.c_void_p), ("s", ctypes.c_void_p), ("rows", ctypes.c_uint32),
                 ("cols", ctypes.c_uint32)]
@@ -78,6 +84,8 @@ def oracle():
         _float_sigs(l, "pko_", [])
         l.pko_conformer_layer.argtypes = [ctypes.POINTER(Layer), ctypes.c_void_p, ctypes.c_uint32,
                                           ctypes.POINTER(Act), ctypes.c_uint32, ctypes.c_int]
+        l.pko_conformer_layer_with.argtypes = [ctypes.POINTER(Kernels), ctypes.POINTER(Layer), ctypes.c_void_p,
+                                               ctypes.c_uint32, ctypes.POINTER(Act), ctypes.c_uint32, ctypes.c_int]
         _oracle = l
     return _oracle
 
@@ -95,6 +103,7 @@ def ref():
         l.pkref_quantize_threads.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(Act),
                                              ctypes.c_void_p, ctypes.c_size_t]
         _float_sigs(l, "pkref_", [ctypes.c_int])
+        l.pkref_kernels.argtypes = [ctypes.c_int, ctypes.POINTER(Kernels)]
         _ref = l
     return _ref
 
@@ -229,11 +238,12 @@ def gemm_f32(w_panels, ld, rows, n, x, T, bias=None, bs=0, relu=0, impl="oracle"
     return out
 
 
-def conformer_layer(weights, x, T, ape_q, ape_d, qb, threads=8):
+def conformer_layer(weights, x, T, ape_q, ape_d, qb, threads=8, impl="oracle"):
     """pko_conformer_layer on a copy of x [T, D]; weights is a dict of numpy
     arrays (LAYER_NORMS, bias_u, bias_v, dw, dw_b, and for each of LAYER_MATS
     the PK_Q8 panels `name` and row scales `name_s`) with the shapes D, H, F,
-    K and eps. Returns the new x."""
+    K and eps. Returns the new x. impl names a reference backend ("ref",
+    "avx512-vnni") to compose the layer from its kernels instead."""
     L = Layer(D=weights["D"], H=weights["H"], F=weights["F"], K=weights["K"], eps=weights["eps"])
     keep = []
     for n in LAYER_NORMS + ("bias_u", "bias_v", "dw", "dw_b"):
@@ -248,7 +258,13 @@ def conformer_layer(weights, x, T, ape_q, ape_d, qb, threads=8):
     y = _f32(x).copy()
     D = weights["D"]
     a = Act(_p(ape_q), _p(ape_d), D, qb, 2 * T - 1)
-    rc = oracle().pko_conformer_layer(ctypes.byref(L), _p(y), T, ctypes.byref(a), qb, threads)
+    if impl == "oracle":
+        rc = oracle().pko_conformer_layer(ctypes.byref(L), _p(y), T, ctypes.byref(a), qb, threads)
+    else:
+        k = Kernels()
+        ref().pkref_kernels(ref_index(impl), ctypes.byref(k))
+        rc = oracle().pko_conformer_layer_with(ctypes.byref(k), ctypes.byref(L), _p(y), T, ctypes.byref(a), qb,
+                                               threads)
     if rc:
         raise ValueError(f"pko_conformer_layer: {rc}")
     return y

@@ -176,6 +176,22 @@ def test_layer_is_the_references_kernels_composed(T, qb):
     assert np.array_equal(bits(got), bits(want))
 
 
+@needs_ref
+@pytest.mark.parametrize("impl", ["ref", "avx512-vnni"])
+def test_layer_from_the_references_table(impl):
+    """The layer composed from a reference backend's own table (what the CPU
+    baseline times) gives the oracle's bits."""
+    if ol.ref_index(impl) < 0 or not ol.ref().pkref_usable(ol.ref_index(impl)):
+        pytest.skip(f"{impl} not usable on this CPU")
+    g = synth.rng(41)
+    w = layer_weights(g, D=128, H=2, F=256, K=9)
+    x = g.standard_normal((29, 128)).astype(np.float32)
+    _, ape_q, ape_d = positions(g, 29, 128, 32)
+    a = ol.conformer_layer(w, x, 29, ape_q, ape_d, 32, threads=3)
+    b = ol.conformer_layer(w, x, 29, ape_q, ape_d, 32, threads=5, impl=impl)
+    assert np.array_equal(bits(a), bits(b))
+
+
 def test_layer_bits_do_not_depend_on_threads():
     g = synth.rng(99)
     w = layer_weights(g, D=128, H=2, F=256, K=9)
