@@ -38,16 +38,17 @@ __device__ __forceinline__ float lanes16_sum(float v) {
 
 /* The mean and 1 / sqrt(var + eps) of the row x[0, n) (n a multiple of 16)
  * as backend/ref/kernels.c:115-129 computes them, in every lane of a 16-lane
- * group whose lane l is l. */
-__device__ __forceinline__ void row_stats(const float *__restrict__ x, uint32_t n, float eps, uint32_t l,
-                                          float &mean, float &r) {
+ * group whose lane l is l. x is the row staged in LDS: the chains read it
+ * strided, and every read can be in flight before the first add. */
+__device__ __forceinline__ void row_stats(const float *x, uint32_t n, float eps, uint32_t l, float &mean,
+                                          float &r) {
     float acc = 0.0f;
-#pragma unroll 8
+#pragma unroll 16
     for (uint32_t j = l; j < n; j += 16)
         acc += x[j];
     mean = lanes16_sum(acc) / (float)n;
     acc = 0.0f;
-#pragma unroll 8
+#pragma unroll 16
     for (uint32_t j = l; j < n; j += 16) {
         const float c = x[j] - mean;
         acc += c * c;
@@ -62,6 +63,27 @@ __device__ __forceinline__ float4 normed(float4 v, float mean, float r, float4 w
                        (v.w - mean) * r * w.w + b.w);
 }
 
+/* A wave's frame of n <= 256 CH floats: loaded once as float4 chunks
+ * i + 64 c into registers and into the wave's LDS row, then its mean and
+ * 1 / sqrt(var + eps) from the row. */
+template <int CH>
+__device__ __forceinline__ void frame_stats(const float *__restrict__ xr, float *row, uint32_t n, float eps,
+                                            int lane, float4 (&v)[CH], float &mean, float &r) {
+    const uint32_t n4 = n >> 2;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < n4) {
+            v[c] = ((const float4 *)xr)[i];
+            ((float4 *)row)[i] = v[c];
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    row_stats(row, n, eps, lane & 15, mean, r);
+}
+
 /* ------------------------------------------------------------- normq --
  *
  * core/encoder.c:108-128: each frame layer-normed and quantized whole, in
@@ -69,25 +91,26 @@ __device__ __forceinline__ float4 normed(float4 v, float mean, float r, float4 w
  * frame, four frames a workgroup. The row's sums take 16 lanes (their
  * chains are the reference's and cannot be split); the wave's other lanes
  * compute the same chains, which costs nothing on the critical path. Then
- * each lane takes float4 chunks i + 64 c of the row, as the quantizer does. */
+ * each lane normalizes its float4 chunks i + 64 c, as the quantizer holds
+ * them. */
 template <int CH, int QB>
 __global__ __launch_bounds__(256) void normq_kernel(int8_t *__restrict__ qp, float *__restrict__ d,
                                                     const float *__restrict__ x, uint32_t n, uint32_t T,
                                                     const float *__restrict__ w, const float *__restrict__ b,
                                                     float eps) {
-    const int lane = threadIdx.x & 63;
-    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    __shared__ __attribute__((aligned(16))) float rows[4][256 * CH];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.x * 4 + wv;
     if (t >= T)
         return;
-    const float *xr = x + (size_t)t * n;
-    float mean, r;
-    row_stats(xr, n, eps, lane & 15, mean, r);
-    const uint32_t n4 = n >> 2;
     float4 v[CH];
+    float mean, r;
+    frame_stats<CH>(x + (size_t)t * n, rows[wv], n, eps, lane, v, mean, r);
+    const uint32_t n4 = n >> 2;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
-        v[c] = i < n4 ? normed(((const float4 *)xr)[i], mean, r, ((const float4 *)w)[i], ((const float4 *)b)[i])
+        v[c] = i < n4 ? normed(v[c], mean, r, ((const float4 *)w)[i], ((const float4 *)b)[i])
                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     const WaveScales<CH, QB> sc(v);
@@ -113,26 +136,21 @@ template <int CH>
 __global__ __launch_bounds__(256) void norm_kernel(float *__restrict__ x, uint32_t n, uint32_t T,
                                                    const float *__restrict__ w, const float *__restrict__ b,
                                                    float eps) {
-    const int lane = threadIdx.x & 63;
-    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    __shared__ __attribute__((aligned(16))) float rows[4][256 * CH];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.x * 4 + wv;
     if (t >= T)
         return;
     float *xr = x + (size_t)t * n;
-    float mean, r;
-    row_stats(xr, n, eps, lane & 15, mean, r);
-    const uint32_t n4 = n >> 2;
     float4 v[CH];
+    float mean, r;
+    frame_stats<CH>(xr, rows[wv], n, eps, lane, v, mean, r);
+    const uint32_t n4 = n >> 2;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
         if (i < n4)
-            v[c] = normed(((const float4 *)xr)[i], mean, r, ((const float4 *)w)[i], ((const float4 *)b)[i]);
-    }
-#pragma unroll
-    for (int c = 0; c < CH; c++) {
-        const uint32_t i = lane + 64 * c;
-        if (i < n4)
-            ((float4 *)xr)[i] = v[c];
+            ((float4 *)xr)[i] = normed(v[c], mean, r, ((const float4 *)w)[i], ((const float4 *)b)[i]);
     }
 }
 
