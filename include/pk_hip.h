@@ -12,7 +12,7 @@
  * This library computes both on the GPU with the reference's bits: the int8
  * activations, their scales and every fp32 output are those of the
  * reference's scalar ref backend (backend/ref/kernels.c:24-86) on the same
- * inputs. The entry points come in three groups:
+ * inputs. The entry points come in five groups:
  *
  *   1. the drop-in: pk_hip_quantize and pk_hip_gemm_q8 take host pointers and
  *      the arguments of the table's quantize and gemm_q8, and return with the
@@ -21,7 +21,12 @@
  *      into HBM (the reference binds matrices at core/model.c:345-363);
  *   3. the device-resident path: the same two operations on device pointers,
  *      asynchronous on a caller's stream, for callers that keep activations
- *      in HBM.
+ *      in HBM;
+ *   4. the device-resident encoder layer: the passes the reference runs
+ *      between its products, fused with their quantizes, and a whole layer
+ *      in one call (core/encoder.c:108-368);
+ *   5. the decoder's token steps: its T = 1 products fused into one launch a
+ *      step (core/decoder.c:54-101).
  *
  * Every function returns PK_HIP_OK or an error code (pk_hip_strerror names it,
  * pk_hip_last_error gives the calling thread's last message); nothing falls
@@ -260,6 +265,35 @@ size_t pk_hip_layer_workspace(const pk_hip_layer *L, uint32_t T, uint32_t qb);
  * kernels. Calls that overlap on one workspace race. */
 int pk_hip_layer_dev(const pk_hip_layer *L, float *x, uint32_t T, const int8_t *ape_qp, const float *ape_d,
                      uint32_t qb, void *ws, size_t ws_bytes, void *stream);
+
+/* ------------------------------------------ the decoder's token steps --- */
+
+/* The decoder's per-token products (core/decoder.c:54-101), each a quantize
+ * of one row (one block) and a T = 1 product, latency-bound: each entry is
+ * one launch (the joint two) that fuses what the reference runs as separate
+ * calls. Device pointers; the matrices uploaded, cols <= 4096. Same bits as
+ * the reference's calls over its ref kernels. No counterpart in the kernel
+ * table: these are core/decoder.c's steps, for a caller whose prediction
+ * state lives in HBM. */
+
+/* gemv (core/decoder.c:54-63): x (m's cols floats) quantized whole and
+ * multiplied: out[r] for every row r of m, plus bias[r] if bias, added to
+ * out[r] if add. */
+int pk_hip_gemv_dev(float *out, const pk_hip_q8 *m, const float *bias, const float *x, int add, void *stream);
+
+/* One LSTM layer's step (core/decoder.c:68-75): gates = wx x + b, then
+ * + wh h_in (the reference's two calls), then the cell (backend/kernels.h:
+ * 180-187): c stepped in place, the new h to h_out (which must not be h_in).
+ * wx and wh are [4P][P], x, h_in, h_out and c P floats, b 4P. */
+int pk_hip_lstm_step_dev(float *h_out, float *c, const float *h_in, const float *x, const pk_hip_q8 *wx,
+                         const pk_hip_q8 *wh, const float *b, void *stream);
+
+/* The joint (core/decoder.c:81-101): the logits of jout (its rows) from
+ * relu(f + gp) (jout's cols floats each) plus jout_b, and tok_dur[0] = the
+ * first best token of logits [0, V], tok_dur[1] = the first best duration
+ * index among the n_dur logits after them. */
+int pk_hip_joint_dev(float *logit, uint32_t *tok_dur, const pk_hip_q8 *jout, const float *jout_b, const float *f,
+                     const float *gp, uint32_t V, uint32_t n_dur, void *stream);
 
 /* The kernel variant the calling thread launched last, for profiling and
  * tests. */

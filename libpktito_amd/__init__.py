@@ -122,6 +122,10 @@ _SIGS = {
     "pk_hip_attention_dev": (ctypes.c_int, [ctypes.c_void_p] * 7 + [ctypes.c_uint32] * 3 +
                              [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "pk_hip_layer_workspace": (ctypes.c_size_t, [ctypes.POINTER(LayerW), ctypes.c_uint32, ctypes.c_uint32]),
+    "pk_hip_gemv_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_int, ctypes.c_void_p]),
+    "pk_hip_lstm_step_dev": (ctypes.c_int, [ctypes.c_void_p] * 7 + [ctypes.c_void_p]),
+    "pk_hip_joint_dev": (ctypes.c_int, [ctypes.c_void_p] * 6 + [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]),
     "pk_hip_layer_dev": (ctypes.c_int, [ctypes.POINTER(LayerW), ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_size_t,
                                         ctypes.c_void_p]),
@@ -394,3 +398,82 @@ class DeviceLayer:
         for m in self.mats.values():
             m.release()
         self.mats = {}
+
+
+# ------------------------------------------------- the decoder's token steps ---
+
+def gemv_dev(out, m, bias, x, add=0, stream=None):
+    """gemv (core/decoder.c:54-63) on device tensors: x quantized whole, out[r]
+    for every row of the uploaded m."""
+    _check(lib().pk_hip_gemv_dev(_dptr(out), m.handle, _dptr(bias), _dptr(x), int(add), _stream(stream)))
+
+
+def lstm_step_dev(h_out, c, h_in, x, wx, wh, b, stream=None, x_ptr=None):
+    """One LSTM layer's step (core/decoder.c:68-75) on device tensors; x_ptr
+    overrides x (a row of a device embedding)."""
+    _check(lib().pk_hip_lstm_step_dev(_dptr(h_out), _dptr(c), _dptr(h_in), x_ptr if x_ptr is not None else _dptr(x),
+                                      wx.handle, wh.handle, _dptr(b), _stream(stream)))
+
+
+def joint_dev(logit, tok_dur, jout, jout_b, f, gp, V, n_dur, stream=None, f_ptr=None):
+    """The joint (core/decoder.c:81-101) on device tensors: logits and
+    tok_dur (int32 [2]) = (token, duration index)."""
+    _check(lib().pk_hip_joint_dev(_dptr(logit), _dptr(tok_dur), jout.handle, _dptr(jout_b),
+                                  f_ptr if f_ptr is not None else _dptr(f), _dptr(gp), V, n_dur, _stream(stream)))
+
+
+class DeviceDecoder:
+    """The prediction network and joint in HBM (matrices uploaded, vectors as
+    device tensors), from a dict as libpktito_amd.synth.decoder_weights makes;
+    its state (h, c of each layer, two h buffers a layer) stepped on device."""
+
+    def __init__(self, dec, torch):
+        self.torch = torch
+        dev = torch.device("cuda")
+        self.P, self.L, self.J, self.V, self.n_dur = (int(dec[k]) for k in ("P", "L", "J", "V", "n_dur"))
+        f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+        self.embed = f32(dec["embed"])
+        self.m = {}
+        for n in [f"wx{l}" for l in range(self.L)] + [f"wh{l}" for l in range(self.L)] + ["jpred", "jout"]:
+            self.m[n] = Q8Matrix(np.ascontiguousarray(dec[n], dtype=np.int8),
+                                 np.ascontiguousarray(dec[n + "_s"], dtype=np.float32))
+        self.b = [f32(dec[f"b{l}"]) for l in range(self.L)]
+        self.jpred_b, self.jout_b = f32(dec["jpred_b"]), f32(dec["jout_b"])
+        self.h = [[torch.zeros(self.P, dtype=torch.float32, device=dev) for _ in range(2)] for _ in range(self.L)]
+        self.c = [torch.zeros(self.P, dtype=torch.float32, device=dev) for _ in range(self.L)]
+        self.cur = [0] * self.L
+        self.gp = torch.zeros(self.J, dtype=torch.float32, device=dev)
+        self.logit = torch.zeros(self.m["jout"].rows, dtype=torch.float32, device=dev)
+        self.tok_dur = torch.zeros(2, dtype=torch.int32, device=dev)
+
+    def state(self):
+        """(h [L, P], c [L, P]) as the layers hold them now."""
+        h = self.torch.stack([self.h[l][self.cur[l]] for l in range(self.L)])
+        return h, self.torch.stack(self.c)
+
+    def set_state(self, h, c):
+        for l in range(self.L):
+            self.h[l][self.cur[l]].copy_(h[l])
+            self.c[l].copy_(c[l])
+
+    def predict(self, label, stream=None):
+        """core/decoder.c:65-79: the label's embedding through the layers, then
+        gp: L + 1 launches."""
+        x_ptr = self.embed.data_ptr() + 4 * label * self.P
+        for l in range(self.L):
+            hin, hout = self.h[l][self.cur[l]], self.h[l][1 - self.cur[l]]
+            lstm_step_dev(hout, self.c[l], hin, None, self.m[f"wx{l}"], self.m[f"wh{l}"], self.b[l], stream,
+                          x_ptr=x_ptr)
+            self.cur[l] = 1 - self.cur[l]
+            x_ptr = hout.data_ptr()
+        gemv_dev(self.gp, self.m["jpred"], self.jpred_b, self.h[self.L - 1][self.cur[self.L - 1]], 0, stream)
+
+    def joint(self, f, stream=None, f_ptr=None):
+        """core/decoder.c:81-101 at the frame whose encoder half is f."""
+        joint_dev(self.logit, self.tok_dur, self.m["jout"], self.jout_b, f, self.gp, self.V, self.n_dur, stream,
+                  f_ptr=f_ptr)
+
+    def release(self):
+        for m in self.m.values():
+            m.release()
+        self.m = {}

@@ -4,7 +4,8 @@
 
 One hipcc line for gfx950: the kernels (csrc/q8_kernels.hip, the quantizer,
 repack and products; csrc/layer_kernels.hip, the device-resident layer's
-float kernels) and the runtime (csrc/pk_hip.cpp). The flags are part of the path's contract:
+float kernels; csrc/dec_kernels.hip, the decoder's fused per-token launches)
+and the runtime (csrc/pk_hip.cpp). The flags are part of the path's contract:
   -ffp-contract=off    no multiply and add the code writes apart is fused: the
                        epilogue's operations are the reference's, one rounding
                        each (its Makefile builds with the same flag);
@@ -27,7 +28,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libpkhip.so")
-SOURCES = [os.path.join(HERE, "csrc", n) for n in ("q8_kernels.hip", "layer_kernels.hip", "pk_hip.cpp")]
+SOURCES = [os.path.join(HERE, "csrc", n)
+           for n in ("q8_kernels.hip", "layer_kernels.hip", "dec_kernels.hip", "pk_hip.cpp")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

@@ -1,0 +1,237 @@
+/* The decoder's per-token work on the device (core/decoder.c:54-101 in
+ * peterheb/libpktito): its products are T = 1 GEMVs, each a quantize of one
+ * row and a product, latency-bound at a few microseconds of work. Each
+ * launch here fuses what the reference runs as separate calls: the row's
+ * quantize with its product (gemv), an LSTM layer's two products, their add
+ * and its cell (lstm), and the joint's ReLU, quantize, product and argmax.
+ *
+ * Bits: the reference's ref backend's. The quantize is
+ * backend/ref/kernels.c:24-58 with one block of the whole row; the sums are
+ * exact int32 (v_dot4 over the repacked units, any order); the epilogue,
+ * the cell (backend/ref/kernels.c:203-213) and the argmax (the first of
+ * equal values) are the reference's operations in its order. Built with
+ * -ffp-contract=off.
+ */
+#include "q8_device.h"
+#include "q8_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace pkq8 {
+
+constexpr uint32_t kDecMaxCols = 4096;
+
+/* One row of n <= 4096 values quantized whole by one wave into q (LDS,
+ * bytes, zero to a whole number of units); value(k) gives element k. Returns
+ * d (the block rule on magnitude bits: a NaN or an infinity, or an amax
+ * below 2^-121, makes the row zero). */
+template <typename F>
+__device__ __forceinline__ float quant_row(F value, uint32_t n, uint32_t n64, int8_t *q, int lane) {
+    int m = 0;
+    for (uint32_t k = lane; k < n; k += 64)
+        m = max(m, mag_bits(value(k)));
+    const uint32_t mb = (uint32_t)wave_max_nonneg(m);
+    const bool zero = zero_bits(mb);
+    float dv = 0.0f, id = 0.0f;
+    if (!zero) {
+        const float amax = __uint_as_float(mb);
+        dv = amax / 127.0f;
+        id = 127.0f / amax;
+    }
+    for (uint32_t k = lane; k < n64; k += 64)
+        q[k] = (int8_t)(k < n && !zero ? q1(value(k), id) : 0);
+    return dv;
+}
+
+/* The exact int32 sums of the 16 rows of panel p over units [0, kr): lane l
+ * takes row l % 16 and inputs 16 (l / 16) .. + 15 of each unit (the unit's
+ * bytes 16 l .. 16 l + 15: the wave reads each 1 KB unit whole), the four
+ * lanes of a row add up by shuffles. Every lane returns its row's sum. */
+__device__ __forceinline__ int panel_dot(const int8_t *__restrict__ w, uint64_t wstride, uint32_t p, uint32_t kr,
+                                         const int8_t *q, int lane) {
+    int s = 0;
+    const int8_t *wp = w + (size_t)p * kUnitBytes + lane * 16;
+    const int8_t *qp = q + (lane >> 4) * 16;
+#pragma unroll 4
+    for (uint32_t u = 0; u < kr; u++) {
+        const v4i wv = *(const v4i *)(wp + (size_t)u * wstride);
+        const v4i av = *(const v4i *)(qp + 64 * u);
+        s = __builtin_amdgcn_sdot4(wv[0], av[0], s, false);
+        s = __builtin_amdgcn_sdot4(wv[1], av[1], s, false);
+        s = __builtin_amdgcn_sdot4(wv[2], av[2], s, false);
+        s = __builtin_amdgcn_sdot4(wv[3], av[3], s, false);
+    }
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    return s;
+}
+
+/* gemm_q8's epilogue for one output of a one-block row
+ * (backend/ref/kernels.c:75-84): fmaf((float)s, d, +0), times ws, plus the
+ * bias */
+__device__ __forceinline__ float gemv_out(int s, float d, float ws, const float *bias, uint32_t r) {
+    float v = __builtin_fmaf((float)s, d, 0.0f) * ws;
+    if (bias)
+        v = v + bias[r];
+    return v;
+}
+
+/* gemv: a wave a 16-row panel, the row quantized by every wave */
+__global__ __launch_bounds__(64) void gemv_kernel(float *__restrict__ out, const int8_t *__restrict__ w,
+                                                  uint64_t wstride, const float *__restrict__ ws,
+                                                  const float *__restrict__ bias, const float *__restrict__ x,
+                                                  uint32_t n, uint32_t kr, int add) {
+    __shared__ __attribute__((aligned(16))) int8_t q[kDecMaxCols];
+    const int lane = threadIdx.x;
+    const uint32_t p = blockIdx.x;
+    const float d = quant_row([&](uint32_t k) { return x[k]; }, n, 64 * kr, q, lane);
+    __syncthreads();
+    const int s = panel_dot(w, wstride, p, kr, q, lane);
+    if (lane < 16) {
+        const uint32_t r = 16 * p + lane;
+        const float v = gemv_out(s, d, ws[r], bias, r);
+        out[r] = add ? out[r] + v : v;
+    }
+}
+
+/* An LSTM layer's step (core/decoder.c:68-75): a workgroup 16 units j0 ..
+ * j0 + 15, wave w their gate w (rows w P + j), each gate wx x + b and then +
+ * wh h as the reference's two calls make it, then the cell
+ * (backend/ref/kernels.c:203-213). h_in is read, h_out written (other
+ * workgroups still read h_in); c is stepped in place, each unit by one
+ * thread. */
+__global__ __launch_bounds__(256) void lstm_kernel(float *__restrict__ h_out, float *__restrict__ c,
+                                                   const float *__restrict__ h_in, const float *__restrict__ x,
+                                                   const int8_t *__restrict__ wx, const float *__restrict__ wxs,
+                                                   const int8_t *__restrict__ wh, const float *__restrict__ whs,
+                                                   uint64_t wstride, const float *__restrict__ b, uint32_t P,
+                                                   uint32_t kr) {
+    __shared__ __attribute__((aligned(16))) int8_t qx[kDecMaxCols], qh[kDecMaxCols];
+    __shared__ float dq[2], gates[4][16];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t j0 = 16 * blockIdx.x;
+    if (wv == 0) {
+        const float d = quant_row([&](uint32_t k) { return x[k]; }, P, 64 * kr, qx, lane);
+        if (lane == 0)
+            dq[0] = d;
+    } else if (wv == 1) {
+        const float d = quant_row([&](uint32_t k) { return h_in[k]; }, P, 64 * kr, qh, lane);
+        if (lane == 0)
+            dq[1] = d;
+    }
+    __syncthreads();
+    const uint32_t p = (wv * P + j0) / 16;
+    const int sx = panel_dot(wx, wstride, p, kr, qx, lane);
+    const int sh = panel_dot(wh, wstride, p, kr, qh, lane);
+    if (lane < 16) {
+        const uint32_t r = wv * P + j0 + lane;
+        const float g = gemv_out(sx, dq[0], wxs[r], b, r);
+        gates[wv][lane] = g + gemv_out(sh, dq[1], whs[r], nullptr, r);
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const uint32_t t = threadIdx.x, j = j0 + t;
+        const float i = pk_sigmoidf(gates[0][t]);
+        const float f = pk_sigmoidf(gates[1][t]);
+        const float u = pk_tanhf(gates[2][t]);
+        const float o = pk_sigmoidf(gates[3][t]);
+        const float cj = f * c[j] + i * u;
+        c[j] = cj;
+        h_out[j] = o * pk_tanhf(cj);
+    }
+}
+
+/* The joint's logits (core/decoder.c:83-89): z = relu(f + gp) quantized by
+ * every wave, a wave a 16-row panel of jout */
+__global__ __launch_bounds__(64) void joint_kernel(float *__restrict__ logit, const int8_t *__restrict__ w,
+                                                   uint64_t wstride, const float *__restrict__ ws,
+                                                   const float *__restrict__ bias, const float *__restrict__ f,
+                                                   const float *__restrict__ gp, uint32_t J, uint32_t kr) {
+    __shared__ __attribute__((aligned(16))) int8_t q[kDecMaxCols];
+    const int lane = threadIdx.x;
+    const uint32_t p = blockIdx.x;
+    auto z = [&](uint32_t k) {
+        const float v = f[k] + gp[k];
+        return v > 0 ? v : 0.0f;
+    };
+    const float d = quant_row(z, J, 64 * kr, q, lane);
+    __syncthreads();
+    const int s = panel_dot(w, wstride, p, kr, q, lane);
+    if (lane < 16) {
+        const uint32_t r = 16 * p + lane;
+        logit[r] = gemv_out(s, d, ws[r], bias, r);
+    }
+}
+
+/* core/decoder.c:90-98: the first best token of [0, V] and the first best
+ * duration of the n_dur after them. The scan's rule, best = i when
+ * logit[i] > logit[best] from best = 0, picks the first index of the
+ * maximum over the values that are not NaN, unless logit[0] is NaN (nothing
+ * is greater than it). So a lane takes a contiguous run and keeps its first
+ * maximum over non-NaN values, the runs meet in order (ties to the earlier
+ * run, +0 and -0 equal as the comparison has them), and a NaN at 0 wins.
+ * The durations are few: lane 0 scans them. */
+__global__ __launch_bounds__(64) void argmax_kernel(uint32_t *__restrict__ tok_dur, const float *__restrict__ logit,
+                                                    uint32_t V, uint32_t n_dur) {
+    const int lane = threadIdx.x;
+    const uint32_t n = V + 1, run = (n + 63) / 64, a = lane * run, e = a + run < n ? a + run : n;
+    float bv = 0.0f;
+    int bi = -1;
+    for (uint32_t i = a; i < e; i++) {
+        const float v = logit[i];
+        if (v == v && (bi < 0 || v > bv)) {
+            bv = v;
+            bi = (int)i;
+        }
+    }
+    for (int off = 1; off < 64; off <<= 1) {
+        const float ov = __shfl_down(bv, off);
+        const int oi = __shfl_down(bi, off);
+        const bool take = lane + off < 64 && oi >= 0 && (bi < 0 || ov > bv);
+        if (take) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        const float l0 = logit[0];
+        const uint32_t best = l0 != l0 || bi < 0 ? 0u : (uint32_t)bi;
+        uint32_t bd = 0;
+        for (uint32_t i = 1; i < n_dur; i++)
+            if (logit[V + 1 + i] > logit[V + 1 + bd])
+                bd = i;
+        tok_dur[0] = best;
+        tok_dur[1] = bd;
+    }
+}
+
+/* ---------------------------------------------------------- launchers -- */
+
+int launch_gemv(float *out, const int8_t *w, uint64_t wstride, const float *ws, const float *bias, const float *x,
+                uint32_t rows, uint32_t n, uint32_t kr, int add, hipStream_t s) {
+    if (n == 0 || n > kDecMaxCols || rows % 16 || 64 * kr > kDecMaxCols)
+        return -2;
+    gemv_kernel<<<rows / 16, 64, 0, s>>>(out, w, wstride, ws, bias, x, n, kr, add);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_lstm(float *h_out, float *c, const float *h_in, const float *x, const int8_t *wx, const float *wxs,
+                const int8_t *wh, const float *whs, uint64_t wstride, const float *b, uint32_t P, uint32_t kr,
+                hipStream_t s) {
+    if (P == 0 || P % 16 || P > kDecMaxCols || 64 * kr > kDecMaxCols)
+        return -2;
+    lstm_kernel<<<P / 16, 256, 0, s>>>(h_out, c, h_in, x, wx, wxs, wh, whs, wstride, b, P, kr);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstride, const float *ws,
+                 const float *bias, const float *f, const float *gp, uint32_t rows, uint32_t J, uint32_t kr,
+                 uint32_t V, uint32_t n_dur, hipStream_t s) {
+    if (J == 0 || J > kDecMaxCols || rows % 16 || 64 * kr > kDecMaxCols || V + 1 + n_dur > rows || n_dur == 0)
+        return -2;
+    joint_kernel<<<rows / 16, 64, 0, s>>>(logit, w, wstride, ws, bias, f, gp, J, kr);
+    argmax_kernel<<<1, 64, 0, s>>>(tok_dur, logit, V, n_dur);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace pkq8

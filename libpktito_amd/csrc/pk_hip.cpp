@@ -993,4 +993,58 @@ int pk_hip_layer_dev(const pk_hip_layer *L, float *x, uint32_t T, const int8_t *
     return PK_HIP_OK;
 }
 
+/* ------------------------------------------ the decoder's token steps --- */
+
+int pk_hip_gemv_dev(float *out, const pk_hip_q8 *m, const float *bias, const float *x, int add, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!m)
+        return fail(PK_HIP_ENOTUP, "gemv_dev: no matrix");
+    if (!out || !x || m->cols > 4096)
+        return fail(PK_HIP_EINVAL, "gemv_dev: out and x set, cols <= 4096");
+    PK_LAUNCH(pkq8::launch_gemv(out, m->w, (uint64_t)(m->rows / 16) * pkq8::kUnitBytes, m->s, bias, x, m->rows,
+                                m->cols, pkq8::units_with_data(m->cols), add, (hipStream_t)stream),
+              "gemv launch");
+    g_kernel = "gemv";
+    return PK_HIP_OK;
+}
+
+int pk_hip_lstm_step_dev(float *h_out, float *c, const float *h_in, const float *x, const pk_hip_q8 *wx,
+                         const pk_hip_q8 *wh, const float *b, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!wx || !wh)
+        return fail(PK_HIP_ENOTUP, "lstm_step_dev: no matrix");
+    const uint32_t P = wx->cols;
+    if (wx->rows != 4 * P || wh->rows != 4 * P || wh->cols != P || P % 16 || P > 4096)
+        return fail(PK_HIP_EINVAL, "lstm_step_dev: wx and wh [4P][P], P a multiple of 16 up to 4096");
+    if (!h_out || !c || !h_in || !x || !b || h_out == h_in)
+        return fail(PK_HIP_EINVAL, "lstm_step_dev: every pointer set, h_out not h_in");
+    PK_LAUNCH(pkq8::launch_lstm(h_out, c, h_in, x, wx->w, wx->s, wh->w, wh->s,
+                                (uint64_t)(wx->rows / 16) * pkq8::kUnitBytes, b, P, pkq8::units_with_data(P),
+                                (hipStream_t)stream),
+              "lstm launch");
+    g_kernel = "lstm";
+    return PK_HIP_OK;
+}
+
+int pk_hip_joint_dev(float *logit, uint32_t *tok_dur, const pk_hip_q8 *jout, const float *jout_b, const float *f,
+                     const float *gp, uint32_t V, uint32_t n_dur, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!jout)
+        return fail(PK_HIP_ENOTUP, "joint_dev: no matrix");
+    if (!logit || !tok_dur || !f || !gp || jout->cols > 4096 || n_dur == 0 || V + 1 + n_dur > jout->rows)
+        return fail(PK_HIP_EINVAL, "joint_dev: every pointer set, cols <= 4096, V + 1 + n_dur <= rows");
+    PK_LAUNCH(pkq8::launch_joint(logit, tok_dur, jout->w, (uint64_t)(jout->rows / 16) * pkq8::kUnitBytes, jout->s,
+                                 jout_b, f, gp, jout->rows, jout->cols, pkq8::units_with_data(jout->cols), V, n_dur,
+                                 (hipStream_t)stream),
+              "joint launch");
+    g_kernel = "joint";
+    return PK_HIP_OK;
+}
+
 }  // extern "C"

@@ -144,6 +144,24 @@ __device__ __forceinline__ float pk_sigmoidf(float x) { return 1.0f / (1.0f + pk
 /* x * sigmoid(x): SiLU (backend/ref/kernels.c:149-151) */
 __device__ __forceinline__ float pk_silu(float x) { return x * pk_sigmoidf(x); }
 
+/* core/vmath.h:153-166 with its constants (core/vmath.h:104-116): below
+ * |x| = 0.625, x + x^3 p(x^2) with p by Horner's rule in FMAs; above it
+ * 1 - 2 / (e^2|x| + 1) with the sign of x. */
+__device__ __forceinline__ float pk_tanhf(float x) {
+    const float a = __builtin_fabsf(x);
+    if (a < 0.625f) {
+        const float x2 = x * x;
+        float p = -0x1.75e1cep-8f;
+        p = __builtin_fmaf(p, x2, 0x1.52269cp-6f);
+        p = __builtin_fmaf(p, x2, -0x1.b83c5ap-5f);
+        p = __builtin_fmaf(p, x2, 0x1.110726p-3f);
+        p = __builtin_fmaf(p, x2, -0x1.555532p-2f);
+        return __builtin_fmaf(x * x2, p, x);
+    }
+    const float e = pk_expf(2.0f * a);
+    return __builtin_copysignf(1.0f - 2.0f / (e + 1.0f), x);
+}
+
 }  // namespace pkq8
 
 #endif

@@ -105,6 +105,17 @@ int launch_attention(float *of, float *ws, const float *qf, const float *kf, con
 int launch_dwq(int8_t *qp, float *d, const float *u, uint32_t T, uint32_t D, const float *w, const float *b,
                uint32_t K, uint32_t qb, hipStream_t s);
 
+/* The decoder's fused per-token launches (dec_kernels.hip): w the device
+ * units of a matrix (wstride its panels x 1 KB), kr its units with data. */
+int launch_gemv(float *out, const int8_t *w, uint64_t wstride, const float *ws, const float *bias, const float *x,
+                uint32_t rows, uint32_t n, uint32_t kr, int add, hipStream_t s);
+int launch_lstm(float *h_out, float *c, const float *h_in, const float *x, const int8_t *wx, const float *wxs,
+                const int8_t *wh, const float *whs, uint64_t wstride, const float *b, uint32_t P, uint32_t kr,
+                hipStream_t s);
+int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstride, const float *ws,
+                 const float *bias, const float *f, const float *gp, uint32_t rows, uint32_t J, uint32_t kr,
+                 uint32_t V, uint32_t n_dur, hipStream_t s);
+
 /* One product; table->nseg == 1 for a plain call. */
 int launch_gemm(const GemmArgs &g, const SegTable &table, hipStream_t s, const char **name);
 

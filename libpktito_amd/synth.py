@@ -158,3 +158,34 @@ def layer_weights(g, D, H, F, K, eps=1e-5):
     w["dw_b"] = 0.1 * g.standard_normal(D)
     return {k: (v.astype(np.float32) if isinstance(v, np.ndarray) and v.dtype == np.float64 else v)
             for k, v in w.items()}
+
+
+def decoder_weights(g, P=640, L=2, J=640, V=1024, n_dur=5):
+    """Seeded random weights of the prediction network and joint
+    (core/model.h:57-60, 124-131) as a dict of numpy arrays: the label
+    embedding [V + 1, P]; for each LSTM layer l, wx{l} and wh{l} [4P, P] as
+    PK_Q8 bytes with row scales (_s) and the summed biases b{l}; jpred [J, P]
+    and jout [n_out_pad, J] with scales and biases, jout's rows past V + 1 +
+    n_dur zero (the model pads them to 16); and the shapes."""
+    n_out = V + 1 + n_dur
+    n_pad = (n_out + 15) // 16 * 16
+    d = {"P": P, "L": L, "J": J, "V": V, "n_dur": n_dur}
+    d["embed"] = (0.5 * g.standard_normal((V + 1, P))).astype(np.float32)
+
+    def mat(name, rows, cols, live=None):
+        w = weights(g, rows, cols)
+        if live is not None:
+            w[live:] = 0
+        d[name] = pack_q8(w)
+        d[name + "_s"] = (g.uniform(0.5, 1.5, rows) / (127.0 * np.sqrt(cols))).astype(np.float32)
+    for l in range(L):
+        mat(f"wx{l}", 4 * P, P)
+        mat(f"wh{l}", 4 * P, P)
+        d[f"b{l}"] = (0.1 * g.standard_normal(4 * P)).astype(np.float32)
+    mat("jpred", J, P)
+    d["jpred_b"] = (0.1 * g.standard_normal(J)).astype(np.float32)
+    mat("jout", n_pad, J, live=n_out)
+    jb = (0.1 * g.standard_normal(n_pad)).astype(np.float32)
+    jb[n_out:] = 0
+    d["jout_b"] = jb
+    return d

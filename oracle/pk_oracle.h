@@ -34,6 +34,13 @@
  *                             (att_item), 321-368 (ff, layer);
  *                             core/passes.c:164-236 (the attention's panels)
  *
+ * and in pk_oracle_dec.c, the decoder's per-token work:
+ *
+ *   pko_tanhf                 core/vmath.h:153-166
+ *   pko_lstm                  backend/ref/kernels.c:203-213
+ *   pko_gemv_with, pko_predict_with, pko_joint_with
+ *                             core/decoder.c:54-101
+ *
  * How each is pinned, beyond restating the formula:
  *   - against the reference's own compiled ref backend (oracle/_ref, built
  *     from the reference's sources by oracle/Makefile) on seeded cases;
@@ -147,6 +154,7 @@ typedef struct {
     void (*glu)(float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t n);
     void (*dwconv)(float *out, size_t os, const float *x, size_t xs, uint32_t T, uint32_t C,
                    const float *w, const float *b, uint32_t K);
+    void (*lstm)(float *h, float *c, const float *g, uint32_t H);
 } pko_kernels;
 
 extern const pko_kernels pko_kernels_oracle;
@@ -161,6 +169,45 @@ int   pko_conformer_layer(const pko_layer *L, float *x, uint32_t T, const pko_ac
                           int nthreads);
 int   pko_conformer_layer_with(const pko_kernels *k, const pko_layer *L, float *x, uint32_t T,
                                const pko_act *ape, uint32_t qb, int nthreads);
+
+/* ------------------------------------------------------- the decoder --- */
+
+float pko_tanhf(float x);
+void  pko_tanhf_n(float *y, const float *x, size_t n);
+void  pko_lstm(float *h, float *c, const float *g, uint32_t H);
+
+/* An LSTM layer (core/model.h:57-60): wx, wh [4P][P], b the biases summed. */
+typedef struct {
+    pko_q8 wx, wh;
+    const float *b;
+} pko_lstmw;
+
+/* The prediction network and joint (core/model.h:124-131): P = pred_hidden,
+ * L layers, J = joint_hidden, V = vocab (blank among [0, V]), n_dur
+ * durations after the V + 1 token logits; jout has rows >= V + 1 + n_dur. */
+typedef struct {
+    uint32_t P, L, J, V, n_dur;
+    const float *embed;            /* [V + 1][P] */
+    const pko_lstmw *lstm;         /* [L] */
+    pko_q8 jpred;
+    const float *jpred_b;
+    pko_q8 jout;
+    const float *jout_b;
+} pko_decoder;
+
+/* core/decoder.c:54-101: gemv (one row quantized, a T = 1 product),
+ * predict (the LSTM layers stepped in place, h and c L x P, then gp) and
+ * joint (the logits and the first best token and duration). Scratch: q
+ * max(P, J) bytes, gates 4P floats, z J floats, logit jout's rows. */
+void  pko_gemv_with(const pko_kernels *k, int8_t *q, float *d, float *out, const pko_q8 *w, const float *bias,
+                    const float *x, int add);
+void  pko_predict_with(const pko_kernels *k, const pko_decoder *m, uint32_t label, float *h, float *c,
+                       float *gates, int8_t *q, float *gp);
+void  pko_joint_with(const pko_kernels *k, const pko_decoder *m, const float *f, const float *gp, float *z,
+                     int8_t *q, float *logit, uint32_t *tok, uint32_t *dur);
+void  pko_predict(const pko_decoder *m, uint32_t label, float *h, float *c, float *gates, int8_t *q, float *gp);
+void  pko_joint(const pko_decoder *m, const float *f, const float *gp, float *z, int8_t *q, float *logit,
+                uint32_t *tok, uint32_t *dur);
 
 /* kcheck's generator: xorshift64*, state kept by the caller. */
 uint32_t pko_rnd(uint64_t *s);

@@ -156,7 +156,7 @@ void pko_dwconv(float *out, size_t os, const float *x, size_t xs, uint32_t T, ui
 
 /* The oracle's own kernels, as a table */
 const pko_kernels pko_kernels_oracle = {
-    pko_quantize, pko_gemm_q8, pko_gemm_f32, pko_layernorm, pko_softmax, pko_silu, pko_glu, pko_dwconv,
+    pko_quantize, pko_gemm_q8, pko_gemm_f32, pko_layernorm, pko_softmax, pko_silu, pko_glu, pko_dwconv, pko_lstm,
 };
 
 static uint32_t up16(uint32_t x) { return (x + 15) & ~15u; }

@@ -120,4 +120,13 @@ void pkref_kernels(int i, pko_kernels *k) {
     k->silu = t->silu;
     k->glu = t->glu;
     k->dwconv = t->dwconv;
+    k->lstm = t->lstm;
 }
+
+/* The reference's inline tanh (core/vmath.h:153-166) over an array */
+void pkref_tanhf_n(float *y, const float *x, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        y[i] = pk_tanhf(x[i]);
+}
+
+void pkref_lstm(int i, float *h, float *c, const float *g, uint32_t H) { tables[i]->lstm(h, c, g, H); }

@@ -38,12 +38,14 @@ def _float_sigs(l, pre, first):
     getattr(l, pre + "silu").argtypes = first + [_P, _Z]
     getattr(l, pre + "glu").argtypes = first + [_P, _Z, _P, _Z, _U, _U]
     getattr(l, pre + "dwconv").argtypes = first + [_P, _Z, _P, _Z, _U, _U, _P, _P, _U]
+    getattr(l, pre + "tanhf_n").argtypes = [_P, _P, _Z]
+    getattr(l, pre + "lstm").argtypes = first + [_P, _P, _P, _U]
 
 
 class Kernels(ctypes.Structure):
     """pko_kernels: the calls a layer makes, as function pointers."""
     _fields_ = [(n, ctypes.c_void_p) for n in ("quantize", "gemm_q8", "gemm_f32", "layernorm", "softmax", "silu",
-                                               "glu", "dwconv")]
+                                               "glu", "dwconv", "lstm")]
 
 
 class Q8(ctypes.Structure):
@@ -54,6 +56,16 @@ class Q8(ctypes.Structure):
 LAYER_NORMS = ("ff1_nw", "ff1_nb", "att_nw", "att_nb", "conv_nw", "conv_nb", "ff2_nw", "ff2_nb", "out_nw",
                "out_nb")
 LAYER_MATS = ("ff1_up", "ff1_down", "ff2_up", "ff2_down", "q", "k", "v", "pos", "o", "pw1", "pw2")
+
+
+class LstmW(ctypes.Structure):
+    _fields_ = [("wx", Q8), ("wh", Q8), ("b", ctypes.c_void_p)]
+
+
+class Decoder(ctypes.Structure):
+    _fields_ = [("P", _U), ("L", _U), ("J", _U), ("V", _U), ("n_dur", _U), ("embed", ctypes.c_void_p),
+                ("lstm", ctypes.POINTER(LstmW)), ("jpred", Q8), ("jpred_b", ctypes.c_void_p), ("jout", Q8),
+                ("jout_b", ctypes.c_void_p)]
 
 
 class Layer(ctypes.Structure):
@@ -86,6 +98,9 @@ def oracle():
                                           ctypes.POINTER(Act), ctypes.c_uint32, ctypes.c_int]
         l.pko_conformer_layer_with.argtypes = [ctypes.POINTER(Kernels), ctypes.POINTER(Layer), ctypes.c_void_p,
                                                ctypes.c_uint32, ctypes.POINTER(Act), ctypes.c_uint32, ctypes.c_int]
+        l.pko_predict_with.argtypes = [ctypes.POINTER(Kernels), ctypes.POINTER(Decoder), _U, _P, _P, _P, _P, _P]
+        l.pko_joint_with.argtypes = [ctypes.POINTER(Kernels), ctypes.POINTER(Decoder), _P, _P, _P, _P, _P,
+                                     ctypes.POINTER(_U), ctypes.POINTER(_U)]
         _oracle = l
     return _oracle
 
@@ -268,3 +283,80 @@ def conformer_layer(weights, x, T, ape_q, ape_d, qb, threads=8, impl="oracle"):
     if rc:
         raise ValueError(f"pko_conformer_layer: {rc}")
     return y
+
+
+def tanhf(x, impl="oracle"):
+    """core/vmath.h's pk_tanhf over an array."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    (oracle().pko_tanhf_n if impl == "oracle" else ref().pkref_tanhf_n)(_p(y), _p(x), x.size)
+    return y
+
+
+def lstm(h, c, g, impl="oracle"):
+    """pk_k_lstm: new (h, c) from copies of h, c [H] and the gates g [4H]."""
+    h, c = _f32(h).copy(), _f32(c).copy()
+    _float_call("lstm", impl, _p(h), _p(c), _p(_f32(g)), h.size)
+    return h, c
+
+
+def _kernels(impl):
+    k = Kernels()
+    if impl == "oracle":
+        for n, _ in Kernels._fields_:
+            setattr(k, n, ctypes.cast(getattr(oracle(), "pko_" + n), ctypes.c_void_p).value)
+    else:
+        ref().pkref_kernels(ref_index(impl), ctypes.byref(k))
+    return k
+
+
+class DecoderWeights:
+    """The prediction network and joint in the oracle's structure: dec is a
+    dict of numpy arrays (embed [V+1, P]; for each layer l wx{l}, wh{l} PK_Q8
+    bytes with _s scales and b{l}; jpred, jout with _s and _b) and the shapes
+    P, L, J, V, n_dur."""
+
+    def __init__(self, dec):
+        self.keep = []
+
+        def q8(name):
+            q = np.ascontiguousarray(dec[name], dtype=np.int8)
+            s = _f32(dec[name + "_s"])
+            self.keep += [q, s]
+            return Q8(q.ctypes.data, s.ctypes.data, s.size, q.size // s.size)
+
+        def vec(a):
+            a = _f32(a)
+            self.keep.append(a)
+            return a.ctypes.data
+        L = dec["L"]
+        self.layers = (LstmW * L)()
+        for l in range(L):
+            self.layers[l] = LstmW(q8(f"wx{l}"), q8(f"wh{l}"), vec(dec[f"b{l}"]))
+        self.st = Decoder(P=dec["P"], L=L, J=dec["J"], V=dec["V"], n_dur=dec["n_dur"], embed=vec(dec["embed"]),
+                          lstm=self.layers, jpred=q8("jpred"), jpred_b=vec(dec["jpred_b"]), jout=q8("jout"),
+                          jout_b=vec(dec["jout_b"]))
+        self.P, self.L, self.J = dec["P"], L, dec["J"]
+        self.rows = dec["jout_s"].size
+
+
+def predict(dw, label, h, c, impl="oracle"):
+    """core/decoder.c's predict: (new h [L, P], new c [L, P], gp [J])."""
+    h, c = _f32(h).copy(), _f32(c).copy()
+    gates = np.empty(4 * dw.P, np.float32)
+    q = np.empty(max(dw.P, dw.J), np.int8)
+    gp = np.empty(dw.J, np.float32)
+    oracle().pko_predict_with(ctypes.byref(_kernels(impl)), ctypes.byref(dw.st), label, _p(h), _p(c), _p(gates),
+                              _p(q), _p(gp))
+    return h, c, gp
+
+
+def joint(dw, f, gp, impl="oracle"):
+    """core/decoder.c's joint: (logits, token, duration index)."""
+    z = np.empty(dw.J, np.float32)
+    q = np.empty(dw.J, np.int8)
+    logit = np.empty(dw.rows, np.float32)
+    tok, dur = _U(), _U()
+    oracle().pko_joint_with(ctypes.byref(_kernels(impl)), ctypes.byref(dw.st), _p(_f32(f)), _p(_f32(gp)), _p(z),
+                            _p(q), _p(logit), ctypes.byref(tok), ctypes.byref(dur))
+    return logit, tok.value, dur.value

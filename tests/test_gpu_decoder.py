@@ -1,0 +1,215 @@
+"""The decoder's token steps on the GPU against the oracle, bit for bit: the
+fused gemv, an LSTM layer's step (both products, their add and the cell), the
+joint's logits and argmax (including ties, signed zeros and NaNs placed by
+hand), the prediction network over several tokens with its state in HBM,
+and a greedy TDT search (core/decoder.c:104-140) driven the same way over
+the device steps and over the oracle's, which must emit the same tokens."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from libpktito_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return np.where(np.isnan(a), np.float32(np.nan), a).view(np.uint32)
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    assert torch.cuda.is_available()
+    return torch
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.device("cuda"))
+
+
+@pytest.mark.parametrize("rows,cols,add,withbias", [(1040, 640, 0, True), (2560, 640, 0, True), (640, 640, 1, False),
+                                                   (16, 64, 0, False), (48, 4096, 1, True)])
+def test_gemv(hip, torch, rows, cols, add, withbias):
+    g = synth.rng(rows + cols + add)
+    w = synth.pack_q8(synth.weights(g, rows, cols))
+    ws = synth.scales(g, rows)
+    x = (g.standard_normal(cols) * 2).astype(np.float32)
+    bias = g.standard_normal(rows).astype(np.float32) if withbias else None
+    old = g.standard_normal(rows).astype(np.float32)
+    q, d = ol.quantize(x, 1, cols, cols, cols)
+    want = old.copy()
+    ol.gemm_q8(want, 0, w, ws, bias, rows, q, d, cols, cols, 1, add)
+    out = dev(torch, old)
+    say("gemv", rows, cols, add, withbias)
+    with hip.Q8Matrix(w, ws) as m:
+        hip.gemv_dev(out, m, dev(torch, bias) if bias is not None else None, dev(torch, x), add)
+        torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(want))
+
+
+def decoder(seed, model):
+    if model:
+        return synth.decoder_weights(synth.rng(seed))
+    return synth.decoder_weights(synth.rng(seed), P=64, L=2, J=64, V=40, n_dur=5)
+
+
+@pytest.mark.parametrize("model", [False, True])
+def test_predict_over_tokens(hip, torch, model):
+    """The prediction network over a run of labels, its state carried in HBM,
+    against the oracle's predict step by step."""
+    dec = decoder(11, model)
+    dw = ol.DecoderWeights(dec)
+    dd = hip.DeviceDecoder(dec, torch)
+    try:
+        P, L = dec["P"], dec["L"]
+        h = np.zeros((L, P), np.float32)
+        c = np.zeros((L, P), np.float32)
+        for step, label in enumerate([dec["V"] - 1, 0, 5, 5, dec["V"] - 2, 17]):
+            say("predict", model, step, label)
+            dd.predict(label)
+            torch.cuda.synchronize()
+            h, c, gp = ol.predict(dw, label, h, c)
+            dh, dc = dd.state()
+            assert np.array_equal(bits(dh.cpu().numpy()), bits(h)), step
+            assert np.array_equal(bits(dc.cpu().numpy()), bits(c)), step
+            assert np.array_equal(bits(dd.gp.cpu().numpy()), bits(gp)), step
+    finally:
+        dd.release()
+
+
+@pytest.mark.parametrize("model", [False, True])
+def test_joint(hip, torch, model):
+    dec = decoder(12, model)
+    dw = ol.DecoderWeights(dec)
+    dd = hip.DeviceDecoder(dec, torch)
+    try:
+        g = synth.rng(13)
+        for i in range(6):
+            f, gp = (g.standard_normal((2, dec["J"])) * (1 + i)).astype(np.float32)
+            logit, tok, dur = ol.joint(dw, f, gp)
+            dd.gp.copy_(dev(torch, gp))
+            say("joint", model, i)
+            dd.joint(dev(torch, f))
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(dd.logit.cpu().numpy()), bits(logit)), i
+            assert tuple(dd.tok_dur.cpu().numpy().tolist()) == (tok, dur), i
+    finally:
+        dd.release()
+
+
+def test_argmax_rule(hip, torch):
+    """Logits placed through the bias of a zero joint matrix: ties go to the
+    first, +0 and -0 are equal, a NaN never wins but at index 0, where
+    nothing beats it; spread over the lanes' runs (V = 1024)."""
+    dec = decoder(14, True)
+    V, n_dur = dec["V"], dec["n_dur"]
+    dec["jout"] = np.zeros_like(dec["jout"])
+    rows = dec["jout_s"].size
+    f = np.zeros(dec["J"], np.float32)
+    cases = []
+    b = np.zeros(rows, np.float32)
+    b[17] = b[900] = 3.0
+    b[V + 1 + 2] = b[V + 1 + 4] = 1.0
+    cases.append(b.copy())
+    b = np.zeros(rows, np.float32)
+    b[0] = -0.0
+    b[600] = 0.0
+    cases.append(b.copy())
+    b = np.full(rows, -1.0, np.float32)
+    b[2] = np.nan
+    b[16] = np.nan
+    b[17] = 0.5
+    b[1000] = 0.5
+    cases.append(b.copy())
+    b = np.full(rows, -1.0, np.float32)
+    b[0] = np.nan
+    b[700] = 0.5
+    cases.append(b.copy())
+    b = np.full(rows, np.nan, np.float32)
+    cases.append(b.copy())
+    b = (synth.rng(15).standard_normal(rows)).astype(np.float32)
+    b[1024] = b[:V + 1].max()
+    cases.append(b.copy())
+    for k, bias in enumerate(cases):
+        dec["jout_b"] = bias
+        dw = ol.DecoderWeights(dec)
+        _, tok, dur = ol.joint(dw, f, f)
+        dd = hip.DeviceDecoder(dec, torch)
+        try:
+            say("argmax case", k)
+            dd.joint(dev(torch, f))
+            torch.cuda.synchronize()
+            assert tuple(dd.tok_dur.cpu().numpy().tolist()) == (tok, dur), k
+        finally:
+            dd.release()
+
+
+def search(T, predict, joint, blank, durs, max_symbols):
+    """core/decoder.c:104-140, TDT's greedy search, over predict(label) and
+    joint(t) -> (token, duration index)."""
+    toks = []
+    predict(blank)
+    t, last, lasts = 0, None, 0
+    while t < T:
+        while True:
+            at = t
+            k, di = joint(t)
+            d = durs[di]
+            if k == blank and d == 0:
+                d = 1
+            t += d
+            if not (k == blank and t < T):
+                break
+        if k == blank:
+            break
+        toks.append((k, at, durs[di]))
+        lasts = lasts + 1 if last == at else 1
+        last = at
+        predict(k)
+        if lasts >= max_symbols and last == t:
+            t += 1
+    return toks
+
+
+def test_greedy_search_on_device(hip, torch):
+    """The search over 60 encoder frames with the device's steps and with the
+    oracle's: the same tokens, frames and durations."""
+    dec = decoder(16, True)
+    V, J, L, P = dec["V"], dec["J"], dec["L"], dec["P"]
+    durs = [0, 1, 2, 3, 4]
+    T = 60
+    g = synth.rng(17)
+    frames = (g.standard_normal((T, J)) * 2).astype(np.float32)
+    blank = V
+    dw = ol.DecoderWeights(dec)
+    st = {"h": np.zeros((L, P), np.float32), "c": np.zeros((L, P), np.float32), "gp": None}
+
+    def o_predict(k):
+        st["h"], st["c"], st["gp"] = ol.predict(dw, k, st["h"], st["c"])
+
+    def o_joint(t):
+        _, k, di = ol.joint(dw, frames[t], st["gp"])
+        return k, di
+    want = search(T, o_predict, o_joint, blank, durs, 10)
+    dd = hip.DeviceDecoder(dec, torch)
+    try:
+        fd = dev(torch, frames)
+
+        def d_joint(t):
+            dd.joint(None, f_ptr=fd.data_ptr() + 4 * t * J)
+            k, di = dd.tok_dur.cpu().numpy().tolist()
+            return k, di
+        say("search", T)
+        got = search(T, dd.predict, d_joint, blank, durs, 10)
+    finally:
+        dd.release()
+    assert got == want and len(want) > 3
