@@ -246,7 +246,7 @@ def check_replay(pk, torch, prods, graph):
 
 
 def encoder_sweep(pk, torch, M, seed):
-    """24 layers with independent weights (~0.6 GB of int8 in HBM),
+    """The 24-layer encoder's products: with independent weights (~0.6 GB of int8 in HBM),
     each product's input the previous product's fp32 output re-quantized per
     row, in the order ff1_up, ff1_down, q (k and v multiply q's activation and
     go to one launch with the positions' projection), o (on v's output), pw1
@@ -305,7 +305,7 @@ def encoder_sweep(pk, torch, M, seed):
 
 
 def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20):
-    """M in {1, 4, 16} rows through weights rotated over more than
+    """Skinny products: M in {1, 4, 16} rows through weights rotated over more than
     512 MB of distinct matrices, so that L2 and the 256 MB MALL serve none of
     them. One graph of launches over the copies; GB/s from the algorithmic
     bytes N K + 4 N + M K + 4 M + 4 M N of each launch."""
@@ -422,6 +422,64 @@ def device_layer(pk, torch, M, qb, reps=20, warmup=3):
     lay.release()
     del gph
     return ms * 1e3, (w, x, ape)
+
+
+def decoder_steps(pk, torch, with_cpu, cpu_seconds=2.0):
+    """The decoder's token steps (core/decoder.c:54-101) at the model's shapes
+    (pred_hidden 640, 2 LSTM layers, joint 640, vocabulary 1024 + blank, 5
+    durations): a prediction (one token's L + 1 launches) and a joint (two
+    launches) each captured in a HIP graph and replayed; the joint with the
+    readback of its token and duration that a host-driven search needs each
+    step; and the same steps on one host core from the reference's fastest
+    kernels (the reference splits only products of 2048 rows or more, over
+    at most 4 threads)."""
+    from libpktito_amd import synth
+    dec = synth.decoder_weights(synth.rng(90))
+    dd = pk.DeviceDecoder(dec, torch)
+    J = dec["J"]
+    f = torch.from_numpy((synth.rng(91).standard_normal(J) * 2).astype(np.float32)).cuda()
+    out = {}
+    gp = graph_of(torch, lambda: dd.predict(5))
+    out["predict_us"] = round(time_graph(torch, gp, 200, 10) * 1e3, 2)
+    gj = graph_of(torch, lambda: dd.joint(f))
+    out["joint_us"] = round(time_graph(torch, gj, 200, 10) * 1e3, 2)
+    reps = 200
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        dd.joint(f)
+        dd.tok_dur.cpu()
+    out["joint_with_readback_us"] = round((time.perf_counter() - t0) / reps * 1e6, 2)
+    out["launches"] = dict(predict=dec["L"] + 1, joint=2)
+    dd.release()
+    del gp, gj
+    if with_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_lib as ol
+        impl = "oracle"
+        if ol.ref() is not None:
+            for bid in ("avx512-vnni", "avx2-vnni"):
+                i = ol.ref_index(bid)
+                if i >= 0 and ol.ref().pkref_usable(i):
+                    impl = bid
+                    break
+        dw = ol.DecoderWeights(dec)
+        h = np.zeros((dec["L"], dec["P"]), np.float32)
+        c = np.zeros_like(h)
+        fh = f.cpu().numpy()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds / 2:
+            h, c, g = ol.predict(dw, 5, h, c, impl=impl)
+            n += 1
+        tp = (time.perf_counter() - t0) / n
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds / 2:
+            ol.joint(dw, fh, g, impl=impl)
+            n += 1
+        tj = (time.perf_counter() - t0) / n
+        out["cpu_1_thread"] = dict(backend=impl, predict_us=round(tp * 1e6, 2), joint_us=round(tj * 1e6, 2),
+                                   kind="reference" if impl != "oracle" else "port")
+    return out
 
 
 def cpu_layer(w, x, ape, M, qb, seconds):
@@ -599,7 +657,7 @@ def main():
     extra["device_layer_M750"] = dlayer
 
     if not args.quick:
-        # configs[2]: the long-form layer, M = 7500 (one segment of ten minutes)
+        # the long-form layer, M = 7500 (one segment of ten minutes)
         long_prods = make_layer(pk, torch, 7500, seed=2)
         gl = graph_of(torch, layer_step(pk, long_prods))
         lms = time_graph(torch, gl, 10, 3)
@@ -619,7 +677,7 @@ def main():
         del long_prods, gl
         torch.cuda.empty_cache()
 
-        # configs[2]: a ragged batch of 8 segments (12-60 s), each product one
+        # a ragged batch of 8 segments (12-60 s), each product one
         # grouped launch over the segments (the quantize over their rows at once)
         from libpktito_amd import synth
         lens = synth.ragged_lengths()
@@ -650,7 +708,7 @@ def main():
             p.m.release()
         del rag, grg
 
-        # configs[3]: the 24-layer chained sweep, ms of encoder products per audio-minute
+        # the 24-layer chained sweep, ms of encoder products per audio-minute
         sweep = {}
         for Ms in (750, 7500):
             fn, sops, layers = encoder_sweep(pk, torch, Ms, seed=10 + Ms)
@@ -668,8 +726,12 @@ def main():
             torch.cuda.empty_cache()
         extra["encoder_24_layers"] = sweep
 
-        # configs[4]: skinny shapes against HBM
+        # skinny shapes against HBM
         extra["skinny"] = skinny_rates(pk, torch, [(1024, 4096, 4096), (4096, 1024, 1024), (640, 1040, 1030)])
+
+        # the decoder's token steps in their own fused launches
+        extra["decoder_steps"] = decoder_steps(pk, torch, not args.no_cpu)
+        log("decoder steps done")
 
         log("skinny done")
 

@@ -21,46 +21,66 @@ namespace pkq8 {
 
 constexpr uint32_t kDecMaxCols = 4096;
 
-/* One row of n <= 4096 values quantized whole by one wave into q (LDS,
- * bytes, zero to a whole number of units); value(k) gives element k. Returns
- * d (the block rule on magnitude bits: a NaN or an infinity, or an amax
- * below 2^-121, makes the row zero). */
-template <typename F>
-__device__ __forceinline__ float quant_row(F value, uint32_t n, uint32_t n64, int8_t *q, int lane) {
-    int m = 0;
-    for (uint32_t k = lane; k < n; k += 64)
-        m = max(m, mag_bits(value(k)));
-    const uint32_t mb = (uint32_t)wave_max_nonneg(m);
-    const bool zero = zero_bits(mb);
-    float dv = 0.0f, id = 0.0f;
-    if (!zero) {
-        const float amax = __uint_as_float(mb);
-        dv = amax / 127.0f;
-        id = 127.0f / amax;
-    }
-    for (uint32_t k = lane; k < n64; k += 64)
-        q[k] = (int8_t)(k < n && !zero ? q1(value(k), id) : 0);
-    return dv;
+/* Chunk i (elements 4i .. 4i + 3, 4i < n) of a row of n floats: one float4
+ * load when the row is 16-byte aligned and n a multiple of 4 (AL), else
+ * four loads with zeros past n. */
+template <bool AL>
+__device__ __forceinline__ float4 row4(const float *__restrict__ x, uint32_t i, uint32_t n) {
+    if (AL)
+        return ((const float4 *)x)[i];
+    const uint32_t k = 4 * i;
+    return make_float4(x[k], k + 1 < n ? x[k + 1] : 0.0f, k + 2 < n ? x[k + 2] : 0.0f, k + 3 < n ? x[k + 3] : 0.0f);
 }
 
-/* The exact int32 sums of the 16 rows of panel p over units [0, kr): lane l
- * takes row l % 16 and inputs 16 (l / 16) .. + 15 of each unit (the unit's
- * bytes 16 l .. 16 l + 15: the wave reads each 1 KB unit whole), the four
- * lanes of a row add up by shuffles. Every lane returns its row's sum. */
+/* One row of n <= 256 CH values quantized whole by one wave into q (LDS,
+ * bytes, zero to 64 kr, kr <= 4 CH): every lane loads its chunks i + 64 c
+ * first (value4(i) gives chunk i, zeros past n), so the row costs one
+ * memory round trip. Returns d (the block rule on magnitude bits: a NaN or
+ * an infinity, or an amax below 2^-121, makes the row zero). */
+template <int CH, typename F>
+__device__ __forceinline__ float quant_row(F value4, uint32_t n, uint32_t kr, int8_t *q, int lane) {
+    const uint32_t n4 = (n + 3) >> 2;
+    float4 v[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        v[c] = i < n4 ? value4(i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const WaveScales<CH, 0> sc(v);
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < 16 * kr)
+            ((int *)q)[i] = i < n4 && !sc.zero[0] ? pack4(v[c], sc.id[0]) : 0;
+    }
+    return sc.dv[0];
+}
+
+/* The exact int32 sums of the 16 rows of panel p over units [0, kr), kr <=
+ * KU: lane l takes row l % 16 and inputs 16 (l / 16) .. + 15 of each unit
+ * (the unit's bytes 16 l .. 16 l + 15: the wave reads each 1 KB unit whole,
+ * every unit's load issued before the first sum), the four lanes of a row
+ * add up by shuffles. Every lane returns its row's sum. */
+template <int KU>
 __device__ __forceinline__ int panel_dot(const int8_t *__restrict__ w, uint64_t wstride, uint32_t p, uint32_t kr,
                                          const int8_t *q, int lane) {
-    int s = 0;
     const int8_t *wp = w + (size_t)p * kUnitBytes + lane * 16;
     const int8_t *qp = q + (lane >> 4) * 16;
-#pragma unroll 4
-    for (uint32_t u = 0; u < kr; u++) {
-        const v4i wv = *(const v4i *)(wp + (size_t)u * wstride);
-        const v4i av = *(const v4i *)(qp + 64 * u);
-        s = __builtin_amdgcn_sdot4(wv[0], av[0], s, false);
-        s = __builtin_amdgcn_sdot4(wv[1], av[1], s, false);
-        s = __builtin_amdgcn_sdot4(wv[2], av[2], s, false);
-        s = __builtin_amdgcn_sdot4(wv[3], av[3], s, false);
-    }
+    v4i wv[KU];
+#pragma unroll
+    for (int u = 0; u < KU; u++)
+        if (u < (int)kr)
+            wv[u] = *(const v4i *)(wp + (size_t)u * wstride);
+    int s = 0;
+#pragma unroll
+    for (int u = 0; u < KU; u++)
+        if (u < (int)kr) {
+            const v4i av = *(const v4i *)(qp + 64 * u);
+            s = __builtin_amdgcn_sdot4(wv[u][0], av[0], s, false);
+            s = __builtin_amdgcn_sdot4(wv[u][1], av[1], s, false);
+            s = __builtin_amdgcn_sdot4(wv[u][2], av[2], s, false);
+            s = __builtin_amdgcn_sdot4(wv[u][3], av[3], s, false);
+        }
     s += __shfl_xor(s, 16);
     s += __shfl_xor(s, 32);
     return s;
@@ -76,17 +96,20 @@ __device__ __forceinline__ float gemv_out(int s, float d, float ws, const float 
     return v;
 }
 
-/* gemv: a wave a 16-row panel, the row quantized by every wave */
+/* gemv: a wave a 16-row panel, the row quantized by every wave. CH float4
+ * chunks a lane hold the row (n <= 256 CH), KU units the panel (kr <= KU);
+ * AL as row4's. */
+template <int CH, int KU, bool AL>
 __global__ __launch_bounds__(64) void gemv_kernel(float *__restrict__ out, const int8_t *__restrict__ w,
                                                   uint64_t wstride, const float *__restrict__ ws,
                                                   const float *__restrict__ bias, const float *__restrict__ x,
                                                   uint32_t n, uint32_t kr, int add) {
-    __shared__ __attribute__((aligned(16))) int8_t q[kDecMaxCols];
+    __shared__ __attribute__((aligned(16))) int8_t q[64 * KU];
     const int lane = threadIdx.x;
     const uint32_t p = blockIdx.x;
-    const float d = quant_row([&](uint32_t k) { return x[k]; }, n, 64 * kr, q, lane);
+    const float d = quant_row<CH>([&](uint32_t i) { return row4<AL>(x, i, n); }, n, kr, q, lane);
     __syncthreads();
-    const int s = panel_dot(w, wstride, p, kr, q, lane);
+    const int s = panel_dot<KU>(w, wstride, p, kr, q, lane);
     if (lane < 16) {
         const uint32_t r = 16 * p + lane;
         const float v = gemv_out(s, d, ws[r], bias, r);
@@ -100,29 +123,30 @@ __global__ __launch_bounds__(64) void gemv_kernel(float *__restrict__ out, const
  * (backend/ref/kernels.c:203-213). h_in is read, h_out written (other
  * workgroups still read h_in); c is stepped in place, each unit by one
  * thread. */
+template <int CH, int KU, bool AL>
 __global__ __launch_bounds__(256) void lstm_kernel(float *__restrict__ h_out, float *__restrict__ c,
                                                    const float *__restrict__ h_in, const float *__restrict__ x,
                                                    const int8_t *__restrict__ wx, const float *__restrict__ wxs,
                                                    const int8_t *__restrict__ wh, const float *__restrict__ whs,
                                                    uint64_t wstride, const float *__restrict__ b, uint32_t P,
                                                    uint32_t kr) {
-    __shared__ __attribute__((aligned(16))) int8_t qx[kDecMaxCols], qh[kDecMaxCols];
+    __shared__ __attribute__((aligned(16))) int8_t qx[64 * KU], qh[64 * KU];
     __shared__ float dq[2], gates[4][16];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t j0 = 16 * blockIdx.x;
     if (wv == 0) {
-        const float d = quant_row([&](uint32_t k) { return x[k]; }, P, 64 * kr, qx, lane);
+        const float d = quant_row<CH>([&](uint32_t i) { return row4<AL>(x, i, P); }, P, kr, qx, lane);
         if (lane == 0)
             dq[0] = d;
     } else if (wv == 1) {
-        const float d = quant_row([&](uint32_t k) { return h_in[k]; }, P, 64 * kr, qh, lane);
+        const float d = quant_row<CH>([&](uint32_t i) { return row4<AL>(h_in, i, P); }, P, kr, qh, lane);
         if (lane == 0)
             dq[1] = d;
     }
     __syncthreads();
     const uint32_t p = (wv * P + j0) / 16;
-    const int sx = panel_dot(wx, wstride, p, kr, qx, lane);
-    const int sh = panel_dot(wh, wstride, p, kr, qh, lane);
+    const int sx = panel_dot<KU>(wx, wstride, p, kr, qx, lane);
+    const int sh = panel_dot<KU>(wh, wstride, p, kr, qh, lane);
     if (lane < 16) {
         const uint32_t r = wv * P + j0 + lane;
         const float g = gemv_out(sx, dq[0], wxs[r], b, r);
@@ -143,20 +167,26 @@ __global__ __launch_bounds__(256) void lstm_kernel(float *__restrict__ h_out, fl
 
 /* The joint's logits (core/decoder.c:83-89): z = relu(f + gp) quantized by
  * every wave, a wave a 16-row panel of jout */
+__device__ __forceinline__ float relu_sum(float a, float b) {
+    const float v = a + b;
+    return v > 0 ? v : 0.0f;
+}
+
+template <int CH, int KU, bool AL>
 __global__ __launch_bounds__(64) void joint_kernel(float *__restrict__ logit, const int8_t *__restrict__ w,
                                                    uint64_t wstride, const float *__restrict__ ws,
                                                    const float *__restrict__ bias, const float *__restrict__ f,
                                                    const float *__restrict__ gp, uint32_t J, uint32_t kr) {
-    __shared__ __attribute__((aligned(16))) int8_t q[kDecMaxCols];
+    __shared__ __attribute__((aligned(16))) int8_t q[64 * KU];
     const int lane = threadIdx.x;
     const uint32_t p = blockIdx.x;
-    auto z = [&](uint32_t k) {
-        const float v = f[k] + gp[k];
-        return v > 0 ? v : 0.0f;
+    auto z4 = [&](uint32_t i) {
+        const float4 a = row4<AL>(f, i, J), g = row4<AL>(gp, i, J);
+        return make_float4(relu_sum(a.x, g.x), relu_sum(a.y, g.y), relu_sum(a.z, g.z), relu_sum(a.w, g.w));
     };
-    const float d = quant_row(z, J, 64 * kr, q, lane);
+    const float d = quant_row<CH>(z4, J, kr, q, lane);
     __syncthreads();
-    const int s = panel_dot(w, wstride, p, kr, q, lane);
+    const int s = panel_dot<KU>(w, wstride, p, kr, q, lane);
     if (lane < 16) {
         const uint32_t r = 16 * p + lane;
         logit[r] = gemv_out(s, d, ws[r], bias, r);
@@ -167,28 +197,33 @@ __global__ __launch_bounds__(64) void joint_kernel(float *__restrict__ logit, co
  * duration of the n_dur after them. The scan's rule, best = i when
  * logit[i] > logit[best] from best = 0, picks the first index of the
  * maximum over the values that are not NaN, unless logit[0] is NaN (nothing
- * is greater than it). So a lane takes a contiguous run and keeps its first
- * maximum over non-NaN values, the runs meet in order (ties to the earlier
- * run, +0 and -0 equal as the comparison has them), and a NaN at 0 wins.
- * The durations are few: lane 0 scans them. */
+ * is greater than it). So a lane takes a contiguous run of at most RUN
+ * (loaded at once) and keeps its first maximum over non-NaN values, the runs
+ * meet in order (ties to the earlier run, +0 and -0 equal as the comparison
+ * has them), and a NaN at 0 wins. The durations are few: lane 0 scans them. */
+template <int RUN>
 __global__ __launch_bounds__(64) void argmax_kernel(uint32_t *__restrict__ tok_dur, const float *__restrict__ logit,
                                                     uint32_t V, uint32_t n_dur) {
     const int lane = threadIdx.x;
-    const uint32_t n = V + 1, run = (n + 63) / 64, a = lane * run, e = a + run < n ? a + run : n;
+    const uint32_t n = V + 1, run = (n + 63) / 64, a = lane * run;
+    float lv[RUN];
+#pragma unroll
+    for (int k = 0; k < RUN; k++)
+        lv[k] = k < (int)run && a + k < n ? logit[a + k] : 0.0f;
     float bv = 0.0f;
     int bi = -1;
-    for (uint32_t i = a; i < e; i++) {
-        const float v = logit[i];
-        if (v == v && (bi < 0 || v > bv)) {
+#pragma unroll
+    for (int k = 0; k < RUN; k++) {
+        const float v = lv[k];
+        if (k < (int)run && a + k < n && v == v && (bi < 0 || v > bv)) {
             bv = v;
-            bi = (int)i;
+            bi = (int)(a + k);
         }
     }
     for (int off = 1; off < 64; off <<= 1) {
         const float ov = __shfl_down(bv, off);
         const int oi = __shfl_down(bi, off);
-        const bool take = lane + off < 64 && oi >= 0 && (bi < 0 || ov > bv);
-        if (take) {
+        if (lane + off < 64 && oi >= 0 && (bi < 0 || ov > bv)) {
             bv = ov;
             bi = oi;
         }
@@ -207,30 +242,69 @@ __global__ __launch_bounds__(64) void argmax_kernel(uint32_t *__restrict__ tok_d
 
 /* ---------------------------------------------------------- launchers -- */
 
+static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+/* The row's float4 chunks a lane and the panel's units a wave: up to 1024
+ * inputs in 16 units, or 4096 in 64; float4 loads when the rows are 16-byte
+ * aligned and n a multiple of 4 (al). */
+#define PK_DEC_SIZE(n, kr, al, CALL)                        \
+    do {                                                    \
+        if ((n) <= 1024 && (kr) <= 16) {                    \
+            constexpr int CH = 4, KU = 16;                  \
+            if (al) {                                       \
+                constexpr bool AL = true;                   \
+                CALL;                                       \
+            } else {                                        \
+                constexpr bool AL = false;                  \
+                CALL;                                       \
+            }                                               \
+        } else {                                            \
+            constexpr int CH = 16, KU = 64;                 \
+            if (al) {                                       \
+                constexpr bool AL = true;                   \
+                CALL;                                       \
+            } else {                                        \
+                constexpr bool AL = false;                  \
+                CALL;                                       \
+            }                                               \
+        }                                                   \
+    } while (0)
+
 int launch_gemv(float *out, const int8_t *w, uint64_t wstride, const float *ws, const float *bias, const float *x,
                 uint32_t rows, uint32_t n, uint32_t kr, int add, hipStream_t s) {
-    if (n == 0 || n > kDecMaxCols || rows % 16 || 64 * kr > kDecMaxCols)
+    if (n == 0 || n > kDecMaxCols || rows % 16 || 64 * kr > kDecMaxCols || 64 * kr < n)
         return -2;
-    gemv_kernel<<<rows / 16, 64, 0, s>>>(out, w, wstride, ws, bias, x, n, kr, add);
+    const bool al = n % 4 == 0 && al16(x);
+    PK_DEC_SIZE(n, kr, al,
+                (gemv_kernel<CH, KU, AL><<<rows / 16, 64, 0, s>>>(out, w, wstride, ws, bias, x, n, kr, add)));
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_lstm(float *h_out, float *c, const float *h_in, const float *x, const int8_t *wx, const float *wxs,
                 const int8_t *wh, const float *whs, uint64_t wstride, const float *b, uint32_t P, uint32_t kr,
                 hipStream_t s) {
-    if (P == 0 || P % 16 || P > kDecMaxCols || 64 * kr > kDecMaxCols)
+    if (P == 0 || P % 16 || P > kDecMaxCols || 64 * kr > kDecMaxCols || 64 * kr < P)
         return -2;
-    lstm_kernel<<<P / 16, 256, 0, s>>>(h_out, c, h_in, x, wx, wxs, wh, whs, wstride, b, P, kr);
+    const bool al = al16(x) && al16(h_in);
+    PK_DEC_SIZE(P, kr, al,
+                (lstm_kernel<CH, KU, AL><<<P / 16, 256, 0, s>>>(h_out, c, h_in, x, wx, wxs, wh, whs, wstride, b, P,
+                                                                kr)));
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstride, const float *ws,
                  const float *bias, const float *f, const float *gp, uint32_t rows, uint32_t J, uint32_t kr,
                  uint32_t V, uint32_t n_dur, hipStream_t s) {
-    if (J == 0 || J > kDecMaxCols || rows % 16 || 64 * kr > kDecMaxCols || V + 1 + n_dur > rows || n_dur == 0)
+    if (J == 0 || J > kDecMaxCols || rows % 16 || 64 * kr > kDecMaxCols || 64 * kr < J || V + 1 + n_dur > rows ||
+        n_dur == 0 || V + 1 > 64 * 64)
         return -2;
-    joint_kernel<<<rows / 16, 64, 0, s>>>(logit, w, wstride, ws, bias, f, gp, J, kr);
-    argmax_kernel<<<1, 64, 0, s>>>(tok_dur, logit, V, n_dur);
+    const bool al = J % 4 == 0 && al16(f) && al16(gp);
+    PK_DEC_SIZE(J, kr, al,
+                (joint_kernel<CH, KU, AL><<<rows / 16, 64, 0, s>>>(logit, w, wstride, ws, bias, f, gp, J, kr)));
+    if (V + 1 <= 64 * 32)
+        argmax_kernel<32><<<1, 64, 0, s>>>(tok_dur, logit, V, n_dur);
+    else
+        argmax_kernel<64><<<1, 64, 0, s>>>(tok_dur, logit, V, n_dur);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

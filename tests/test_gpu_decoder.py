@@ -36,9 +36,13 @@ def dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a)).to(torch.device("cuda"))
 
 
-@pytest.mark.parametrize("rows,cols,add,withbias", [(1040, 640, 0, True), (2560, 640, 0, True), (640, 640, 1, False),
-                                                   (16, 64, 0, False), (48, 4096, 1, True)])
-def test_gemv(hip, torch, rows, cols, add, withbias):
+@pytest.mark.parametrize("rows,cols,add,withbias,off", [(1040, 640, 0, True, 0), (2560, 640, 0, True, 0),
+                                                       (640, 640, 1, False, 0), (16, 64, 0, False, 0),
+                                                       (48, 4096, 1, True, 0), (32, 1056, 0, True, 0),
+                                                       (1040, 640, 0, True, 1), (32, 1056, 1, False, 3)])
+def test_gemv(hip, torch, rows, cols, add, withbias, off):
+    """cols 1056 takes the 64-unit kernel; off > 0 puts x off 16-byte
+    alignment (the kernel's four-load rows)."""
     g = synth.rng(rows + cols + add)
     w = synth.pack_q8(synth.weights(g, rows, cols))
     ws = synth.scales(g, rows)
@@ -51,7 +55,8 @@ def test_gemv(hip, torch, rows, cols, add, withbias):
     out = dev(torch, old)
     say("gemv", rows, cols, add, withbias)
     with hip.Q8Matrix(w, ws) as m:
-        hip.gemv_dev(out, m, dev(torch, bias) if bias is not None else None, dev(torch, x), add)
+        xt = dev(torch, np.concatenate([np.zeros(off, np.float32), x]))[off:]
+        hip.gemv_dev(out, m, dev(torch, bias) if bias is not None else None, xt, add)
         torch.cuda.synchronize()
     assert np.array_equal(bits(out.cpu().numpy()), bits(want))
 
@@ -98,7 +103,8 @@ def test_joint(hip, torch, model):
             logit, tok, dur = ol.joint(dw, f, gp)
             dd.gp.copy_(dev(torch, gp))
             say("joint", model, i)
-            dd.joint(dev(torch, f))
+            off = i % 2                     # odd steps: f off 16-byte alignment
+            dd.joint(dev(torch, np.concatenate([np.zeros(off, np.float32), f]))[off:])
             torch.cuda.synchronize()
             assert np.array_equal(bits(dd.logit.cpu().numpy()), bits(logit)), i
             assert tuple(dd.tok_dur.cpu().numpy().tolist()) == (tok, dur), i
