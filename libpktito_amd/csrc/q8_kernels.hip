@@ -11,6 +11,8 @@
  * (a block's scale can be subnormal) or relaxes division.
  */
 #include "q8_internal.h"
+
+#include <cstring>
 #include "q8_device.h"
 
 #include <float.h>
@@ -1259,6 +1261,17 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
     wait_vm<(NS - 1) * LT>();
     __builtin_amdgcn_s_barrier();
     read_set(f0, 0);
+    /* the first set lands before the loop: where the loop's entry copies
+     * registers, it then copies the fragments, not what preceded them */
+    wait_lgkm<0>();
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        asm volatile("" : "+v"(f0.f[r]));
+    if constexpr (BLK != 0) {
+#pragma unroll
+        for (int r = 0; r < TM * BPU; r++)
+            asm volatile("" : "+v"(f0.dv[r]));
+    }
 
     /* steady state: stages [0, ns - NS), each refilling its slot; SPI
      * sub-steps a pass, an even number, so f0 and f1 alternate statically */
@@ -1536,6 +1549,10 @@ static const RingCfg kRing[] = {
     /* three slots: three workgroups a CU */
     { "pipe<64x64,2,3>", 64, 64, 2, 3, 1, run_pipe<2, 2, 2, 2, 2, 3, 1>, run_pipe_batch<2, 2, 2, 2, 2, 3, 1>, run_pipe<2, 2, 2, 2, 2, 3, 1, 1>, run_pipe<2, 2, 2, 2, 2, 3, 1, 2> },
     { "pipe<64x64,2,3,k2>", 64, 64, 2, 3, 2, run_pipe<2, 2, 2, 2, 2, 3, 2>, run_pipe_batch<2, 2, 2, 2, 2, 3, 2>, nullptr, nullptr },
+    /* eight waves of 32 x 16: two a SIMD, so one wave's block chain runs
+     * beside the other's MFMAs where a product has too few tiles for two
+     * workgroups a CU */
+    { "pipe<64x64w8,2,4>", 64, 64, 2, 4, 1, run_pipe<2, 4, 2, 1, 2, 4, 1>, run_pipe_batch<2, 4, 2, 1, 2, 4, 1>, run_pipe<2, 4, 2, 1, 2, 4, 1, 1>, run_pipe<2, 4, 2, 1, 2, 4, 1, 2> },
 };
 constexpr int kNRing = sizeof kRing / sizeof kRing[0];
 
@@ -1589,6 +1606,32 @@ static int pick_ring(uint32_t rows, uint64_t frames, uint32_t ku) {
     if (t64 >= 256 && ku % 8 == 0)
         return 2;
     return ku % 16 == 0 ? 3 : ku % 8 == 0 ? 2 : 1;
+}
+
+static int ring_index(const char *name) {
+    for (int i = 0; i < kNRing; i++)
+        if (!strcmp(kRing[i].name, name))
+            return i;
+    return -1;
+}
+
+/* The tile for a blocked product, measured on the layer's shapes at 750
+ * frames in blocks of 32 and 64: the chip-filling 128 x 128 tile as the
+ * per-column heuristic picks it; else, where 64 x 64 tiles leave CUs
+ * without two workgroups (or the inputs are deep), eight waves of 32 x 16,
+ * two a SIMD, so one wave's block chain runs beside the other's MFMAs; with
+ * two workgroups a CU or more, three slots and three workgroups a CU. */
+static int pick_blocked(uint32_t rows, uint64_t frames, uint32_t ku) {
+    const int c = pick_ring(rows, frames, ku);
+    if (g_forced_ring >= 0 || c == 5)
+        return c;
+    static const int w8 = ring_index("pipe<64x64w8,2,4>"), s3 = ring_index("pipe<64x64,2,3>");
+    const uint64_t t64 = (uint64_t)((rows + 63) / 64) * ((frames + 63) / 64);
+    if ((t64 < 256 || ku >= 32) && w8 >= 0 && fits(w8, ku))
+        return w8;
+    if (t64 >= 512 && s3 >= 0 && fits(s3, ku))
+        return s3;
+    return c;
 }
 
 template <int WN, int WM, int TN, int TM, int MODE>
@@ -1658,7 +1701,7 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
     /* blocks of 64 or 32 inputs (the encoder's modes): the pipelined tile
      * the heuristic picks for these frames, if it has a blocked variant */
     if ((mode == 1 && g.qb == 64) || (mode == 2 && g.qb == 32)) {
-        int c = pick_ring(g.rows, frames, g.ku);
+        int c = pick_blocked(g.rows, frames, g.ku);
         if (!(mode == 1 ? kRing[c].run64 : kRing[c].run32))
             c = fits(6, g.ku) ? 6 : 4;      /* 4 takes any ku: one unit a stage, four slots */
         auto run = mode == 1 ? kRing[c].run64 : kRing[c].run32;
