@@ -1567,8 +1567,6 @@ int set_ring(int i) {
 
 int ring_count() { return kNRing; }
 
-/* The tile for a product of `frames` frames into `rows` channels: the
- * largest that still gives every CU a workgroup. */
 /* whether tiling i takes ku units a panel: ring_tile runs whole passes of
  * four stages; pipe_tile needs its slots' worth of stages to start, and its
  * steady state runs whole passes of max(2, UPS) sub-steps, so with one unit
@@ -1584,30 +1582,6 @@ static bool fits(int i, uint32_t ku) {
     return ns >= c.slots && (c.ups > 1 || (ns - c.slots) % 2 == 0);
 }
 
-static int pick_ring(uint32_t rows, uint64_t frames, uint32_t ku) {
-    if (g_forced_ring >= 0 && fits(g_forced_ring, ku))
-        return g_forced_ring;
-    auto tiles = [&](int i) { return (uint64_t)((rows + kRing[i].bn - 1) / kRing[i].bn) * ((frames + kRing[i].bm - 1) / kRing[i].bm); };
-    /* measured on the layer's shapes at 750 and 7500 frames (every tiling,
-     * every product): a CU's worth of 128 x 128 tiles takes the eight-wave
-     * pipelined tile; fewer take 64 x 64 pipelined tiles of two-unit stages,
-     * split into two K groups where the inputs are deep;
-     * inputs too short for their slots take the ring, 64 x 64, with longer
-     * stages the fewer the tiles */
-    if (tiles(0) >= 256 && fits(5, ku))
-        return 5;
-    if (ku >= 32 && tiles(6) < 512 && fits(13, ku))
-        return 13;          /* deep inputs, few tiles: two K groups a tile */
-    if (fits(6, ku))
-        return 6;
-    const uint64_t t64 = tiles(1);
-    if (t64 >= 512)
-        return 1;
-    if (t64 >= 256 && ku % 8 == 0)
-        return 2;
-    return ku % 16 == 0 ? 3 : ku % 8 == 0 ? 2 : 1;
-}
-
 static int ring_index(const char *name) {
     for (int i = 0; i < kNRing; i++)
         if (!strcmp(kRing[i].name, name))
@@ -1615,22 +1589,46 @@ static int ring_index(const char *name) {
     return -1;
 }
 
-/* The tile for a blocked product, measured on the layer's shapes at 750
- * frames in blocks of 32 and 64: the chip-filling 128 x 128 tile as the
- * per-column heuristic picks it; else, where 64 x 64 tiles leave CUs
- * without two workgroups (or the inputs are deep), eight waves of 32 x 16,
- * two a SIMD, so one wave's block chain runs beside the other's MFMAs; with
- * two workgroups a CU or more, three slots and three workgroups a CU. */
-static int pick_blocked(uint32_t rows, uint64_t frames, uint32_t ku) {
-    const int c = pick_ring(rows, frames, ku);
-    if (g_forced_ring >= 0 || c == 5)
-        return c;
+/* The tile for a product of `frames` frames into `rows` channels. */
+static int pick_ring(uint32_t rows, uint64_t frames, uint32_t ku) {
+    if (g_forced_ring >= 0 && fits(g_forced_ring, ku))
+        return g_forced_ring;
+    auto tiles = [&](int i) { return (uint64_t)((rows + kRing[i].bn - 1) / kRing[i].bn) * ((frames + kRing[i].bm - 1) / kRing[i].bm); };
     static const int w8 = ring_index("pipe<64x64w8,2,4>"), s3 = ring_index("pipe<64x64,2,3>");
-    const uint64_t t64 = (uint64_t)((rows + 63) / 64) * ((frames + 63) / 64);
-    if ((t64 < 256 || ku >= 32) && w8 >= 0 && fits(w8, ku))
+    /* measured on the layer's shapes at 750 and 7500 frames (every tiling,
+     * every product): a CU's worth of 128 x 128 tiles takes the eight-wave
+     * pipelined tile; fewer take 64 x 64 pipelined tiles of two-unit stages:
+     * split into two K groups where the inputs are deep; eight waves of
+     * 32 x 16 (two a SIMD) where the tiles leave CUs idle; three slots
+     * (three workgroups a CU) where there are two tiles a CU or more;
+     * inputs too short for their slots take the ring, 64 x 64, with longer
+     * stages the fewer the tiles */
+    if (tiles(0) >= 256 && fits(5, ku))
+        return 5;
+    if (ku >= 32 && tiles(6) < 512 && fits(13, ku))
+        return 13;          /* deep inputs, few tiles: two K groups a tile */
+    const uint64_t t64 = tiles(1);
+    if (t64 < 256 && w8 >= 0 && fits(w8, ku))
         return w8;
     if (t64 >= 512 && s3 >= 0 && fits(s3, ku))
         return s3;
+    if (fits(6, ku))
+        return 6;
+    if (t64 >= 512)
+        return 1;
+    if (t64 >= 256 && ku % 8 == 0)
+        return 2;
+    return ku % 16 == 0 ? 3 : ku % 8 == 0 ? 2 : 1;
+}
+
+/* The tile for a blocked product: the per-column pick, but deep inputs with
+ * few tiles take the eight-wave tile (the two-K-group tiles have no blocked
+ * build; measured in blocks of 32 and 64 at 750 frames). */
+static int pick_blocked(uint32_t rows, uint64_t frames, uint32_t ku) {
+    static const int w8 = ring_index("pipe<64x64w8,2,4>");
+    const int c = pick_ring(rows, frames, ku);
+    if (g_forced_ring < 0 && c == 13 && w8 >= 0 && fits(w8, ku))
+        return w8;
     return c;
 }
 
