@@ -247,6 +247,47 @@ __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q,
         d[t] = sc.dv[0];
 }
 
+/* Blocks of QB inputs over wide columns (n > 1024): a wave a 1024-input
+ * chunk of a column (S chunks a column), so a product's worth of columns
+ * spreads over S times the waves; a block never straddles chunks, so each
+ * wave's scales are its own. Writes the packed copy (and q when set) and d
+ * as quant_wave_kernel does. */
+template <int QB, int OP>
+__global__ __launch_bounds__(256) void quant_chunk_kernel(int8_t *__restrict__ q, int8_t *__restrict__ qp,
+                                                          float *__restrict__ d, const float *__restrict__ x,
+                                                          size_t xs, uint32_t n, uint32_t T, uint32_t S) {
+    static_assert(QB == 32 || QB == 64, "blocks within a chunk");
+    const int lane = threadIdx.x & 63;
+    const uint32_t w = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t t = w / S, i0 = (w % S) * 256;
+    if (t >= T)
+        return;
+    const uint32_t n4 = n >> 2;
+    const float4 *xr = (const float4 *)(x + (size_t)t * xs);
+    float4 v[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = i0 + lane + 64 * c;
+        v[c] = i < n4 ? quant_in<OP>(xr[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const WaveScales<4, QB> sc(v);
+    int *qr = (int *)(q + (size_t)t * n);
+    const uint32_t G = (T + 15) / 16, g = t >> 4, r = t & 15;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t i = i0 + lane + 64 * c;
+        if (i < n4) {
+            const int v4 = sc.zero[c] ? 0 : pack4(v[c], sc.id[c]);
+            if (q)
+                qr[i] = v4;
+            const uint32_t k = 4 * i;
+            *(int *)(qp + ((size_t)(k >> 6) * G + g) * kUnitBytes + in_unit(k, r)) = v4;
+            if ((i & (QB / 4 - 1)) == 0)
+                d[(size_t)t * (n / QB) + (4 * i) / QB] = sc.dv[c];
+        }
+    }
+}
+
 /* One workgroup of 16 waves a group of 16 columns, for the packed copy of
  * about 7M inputs and more: wave r quantizes column 16 g + r as
  * quant_wave_kernel does, the group's units are put together in LDS, and
@@ -329,6 +370,16 @@ static int launch_quantize_packed_op(int8_t *q, int8_t *qp, float *d, const floa
     } while (0)
     if (qb == n) {
         if (small) PK_QP(4, 0, "<4>"); else PK_QP(16, 0, "<16>");
+    } else if (!small && !group) {
+        /* wide columns in blocks: a wave a 1024-input chunk */
+        const uint32_t S = (n4 + 255) / 256;
+        const uint32_t grid = (uint32_t)(((uint64_t)T * S + 3) / 4);
+        if (qb == 32)
+            quant_chunk_kernel<32, OP><<<grid, 256, 0, s>>>(q, qp, d, x, xs, n, T, S);
+        else
+            quant_chunk_kernel<64, OP><<<grid, 256, 0, s>>>(q, qp, d, x, xs, n, T, S);
+        *name = OP ? (qb == 32 ? "quant_chunk_packed_silu<qb32>" : "quant_chunk_packed_silu<qb64>")
+                   : (qb == 32 ? "quant_chunk_packed<qb32>" : "quant_chunk_packed<qb64>");
     } else if (qb == 32) {
         if (small) PK_QP(4, 32, "<4,qb32>"); else PK_QP(16, 32, "<16,qb32>");
     } else {
