@@ -184,8 +184,9 @@ def force_tiling(index):
 
 def force_quantize(kind):
     """Force the packed quantize's kernel for every later launch (0 one wave
-    a column, 1 one workgroup a 16-column group, -1 automatic); returns the
-    one forced before."""
+    a column, or a wave a 1024-input chunk of a wide column in blocks; 1 one
+    workgroup a 16-column group; 2 one wave a whole column; -1 automatic);
+    returns the one forced before."""
     return lib().pk_hip_force_quantize(kind)
 
 

@@ -70,6 +70,20 @@ __device__ __forceinline__ int mag4(float4 f) {
     return max(max(mag_bits(f.x), mag_bits(f.y)), max(mag_bits(f.z), mag_bits(f.w)));
 }
 
+/* A block's scales from the largest magnitude's bits mb (backend/ref/kernels.c:
+ * 24-58): zero (a NaN or an infinity, or an amax below 2^-121), else d =
+ * amax / 127 and the multiplier 127 / amax. */
+__device__ __forceinline__ void block_scales(uint32_t mb, bool &zero, float &dv, float &id) {
+    zero = zero_bits(mb);
+    dv = 0.0f;
+    id = 0.0f;
+    if (!zero) {
+        const float amax = __uint_as_float(mb);
+        dv = amax / 127.0f;
+        id = 127.0f / amax;
+    }
+}
+
 /* The scales of a column of n <= 4096 inputs that one wave holds, each lane
  * CH float4 chunks of it (chunk c of lane l is float4 l + 64 c, zeros past
  * the column). QB == 0: the column is one block, reduced over the wave;
@@ -81,16 +95,7 @@ struct WaveScales {
     float dv[NB], id[NB];
     bool zero[NB];
 
-    __device__ __forceinline__ void block(int b, uint32_t mb) {
-        zero[b] = zero_bits(mb);
-        dv[b] = 0.0f;
-        id[b] = 0.0f;
-        if (!zero[b]) {
-            const float amax = __uint_as_float(mb);
-            dv[b] = amax / 127.0f;
-            id[b] = 127.0f / amax;
-        }
-    }
+    __device__ __forceinline__ void block(int b, uint32_t mb) { block_scales(mb, zero[b], dv[b], id[b]); }
 
     __device__ __forceinline__ explicit WaveScales(const float4 (&v)[CH]) {
         if constexpr (QB == 0) {

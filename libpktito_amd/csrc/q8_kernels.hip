@@ -348,7 +348,7 @@ static int g_quant_kernel = -1;
 
 int set_quant_kernel(int kind) {
     const int was = g_quant_kernel;
-    g_quant_kernel = kind < 0 || kind > 1 ? -1 : kind;
+    g_quant_kernel = kind < 0 || kind > 2 ? -1 : kind;
     return was;
 }
 
@@ -358,6 +358,8 @@ static int launch_quantize_packed_op(int8_t *q, int8_t *qp, float *d, const floa
     const uint32_t n4 = n / 4;
     const bool small = n4 <= 256;
     const bool group = g_quant_kernel < 0 ? (uint64_t)T * n >= kGroupQuantInputs : g_quant_kernel == 1;
+    /* 2: one wave a whole column also where the column is wide and in blocks */
+    const bool wide = !small && !group && g_quant_kernel != 2;
 #define PK_QP(CH, QB, NAME)                                                                       \
     do {                                                                                          \
         if (group) {                                                                              \
@@ -370,7 +372,7 @@ static int launch_quantize_packed_op(int8_t *q, int8_t *qp, float *d, const floa
     } while (0)
     if (qb == n) {
         if (small) PK_QP(4, 0, "<4>"); else PK_QP(16, 0, "<16>");
-    } else if (!small && !group) {
+    } else if (wide) {
         /* wide columns in blocks: a wave a 1024-input chunk */
         const uint32_t S = (n4 + 255) / 256;
         const uint32_t grid = (uint32_t)(((uint64_t)T * S + 3) / 4);

@@ -332,8 +332,9 @@ def special_rows(x):
                                     (300, 4096, 4096), (300, 4096, 64), (750, 1024, 32), (2000, 4096, 4096),
                                     (1800, 4096, 32), (7500, 1024, 1024), (2249, 4096, 64)])
 def test_packed_quantize_kernels(hip, torch, T, n, qb):
-    """The packed quantize kernels (one wave a column, or a 1024-input chunk
-    of a wide column in blocks; one workgroup a 16-column group) and the
+    """The packed quantize kernels (one wave a column, or a wave a
+    1024-input chunk of a wide column in blocks; one workgroup a 16-column
+    group) and the
     choice by size: q, d and the packed bytes are
     the oracle's, with and without the row-major copy, over a packed buffer
     that held other bytes before."""
@@ -344,7 +345,7 @@ def test_packed_quantize_kernels(hip, torch, T, n, qb):
     xt = torch.from_numpy(x).to(dev)
     big = T * n >= 7 << 20
     try:
-        for kind in (-1, 0, 1):
+        for kind in (-1, 0, 1, 2):
             hip.force_quantize(kind)
             for with_q in (True, False):
                 qt = torch.full((T, n), 77, dtype=torch.int8, device=dev) if with_q else None
@@ -353,7 +354,7 @@ def test_packed_quantize_kernels(hip, torch, T, n, qb):
                 say("packed quantize", T, n, qb, kind, with_q)
                 hip.quantize_packed_dev(qt, qp, dt, xt, n, T, n, qb=qb)
                 torch.cuda.synchronize()
-                want = ("quant_group" if kind == 1 or (kind == -1 and big) else
+                want = ("quant_group" if kind == 1 or (kind == -1 and big) else "quant_wave" if kind == 2 else
                         "quant_chunk" if qb != n and n > 1024 else "quant_wave")
                 assert hip.last_kernel().startswith(want), (kind, hip.last_kernel())
                 if with_q:
