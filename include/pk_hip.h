@@ -314,6 +314,12 @@ int pk_hip_force_tiling(int index);
  * returns the one forced before. All compute the same bits. */
 int pk_hip_force_quantize(int kind);
 
+/* Tests and tuning: the attention's score and PV products for every later
+ * launch in the process: 0 on the matrix cores (one-step fp32 MFMAs, the
+ * default), 1 as VALU fma chains; returns the one set before. Both compute
+ * the same bits. */
+int pk_hip_force_attention(int valu);
+
 #ifdef __cplusplus
 }
 #endif

@@ -83,6 +83,7 @@ _SIGS = {
     "pk_hip_tilings": (ctypes.c_int, []),
     "pk_hip_force_tiling": (ctypes.c_int, [ctypes.c_int]),
     "pk_hip_force_quantize": (ctypes.c_int, [ctypes.c_int]),
+    "pk_hip_force_attention": (ctypes.c_int, [ctypes.c_int]),
     "pk_hip_init": (ctypes.c_int, []),
     "pk_hip_upload_q8": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32]),
     "pk_hip_release_q8": (ctypes.c_int, [ctypes.c_void_p]),
@@ -188,6 +189,13 @@ def force_quantize(kind):
     workgroup a 16-column group; 2 one wave a whole column; -1 automatic);
     returns the one forced before."""
     return lib().pk_hip_force_quantize(kind)
+
+
+def force_attention(valu):
+    """The attention's score and PV products for every later launch: 0 on
+    the matrix cores (the default), 1 as VALU fma chains; returns the one
+    set before."""
+    return lib().pk_hip_force_attention(int(valu))
 
 
 def _ptr(a):

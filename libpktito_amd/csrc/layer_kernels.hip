@@ -409,6 +409,258 @@ __global__ __launch_bounds__(128) void att_pv_kernel(float *__restrict__ of, con
     }
 }
 
+/* ------------------------------------------------- attention on MFMA --
+ *
+ * The same chains on the matrix cores: v_mfma_f32_32x32x1_2b_f32 and
+ * v_mfma_f32_16x16x1_4b_f32 have one input step (K = 1), so each output
+ * takes exactly one product and one add a step, d = fma(a, b, d) with one
+ * rounding (checked against v_fma_f32 on 1.2M outputs of every class of
+ * input: subnormals, both zeros, infinities, NaN, exact cancellation). A
+ * chain of steps in the reference's order is then the reference's fmaf
+ * chain, at the matrix cores' rate and with each operand one register a
+ * lane for 2048 (or 1024) chains.
+ *
+ * 32x32x1_2b: two blocks of 32 x 32; lane l gives A[l / 32][l % 32] and
+ * B[l / 32][l % 32]; output register r of lane l is block r / 16, row
+ * 8 ((r % 16) / 4) + 4 (l / 32) + r % 4, column l % 32.
+ * 16x16x1_4b: four blocks of 16 x 16; lane l gives A[l / 16][l % 16] and
+ * B[l / 16][l % 16]; output register r of lane l is block r / 4, row
+ * 4 (l / 16) + r % 4, column l % 16.
+ *
+ * The scores (content, then the position band added in) and PV, each
+ * with its operands staged through LDS (below). */
+typedef float v32f __attribute__((ext_vector_type(32)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+/* The scores' chains over the head's dimensions, staged through LDS: a
+ * workgroup 64 queries x 128 rows of y (keys; or, BAND, the position rows m
+ * of the band its queries reach), wave (wq, wy) 32 queries x 64 rows on
+ * 32x32x1_2b (its two blocks the two halves of its rows); dimensions in
+ * stages of 16, double-buffered (30 KB: five workgroups a CU), each row's
+ * 16 dimensions contiguous (rows padded to 20 floats: a wave's 16-byte
+ * reads of 16 rows fall in distinct banks), a stage's operands read into
+ * registers before its MFMAs: A = x + bias (one rounding, formed as staged), B = y. Content: S =
+ * the chain. Band: S(i, j) = S(i, j) + the chain of (i, m) for m = T - 1 - i
+ * + j, j a key (each (i, j) one lane's in the grid; the workgroup's rows
+ * start at T - 1 - (i0 + 63), negative at the last query tiles, whose rows
+ * there meet no key). */
+constexpr int kSQ = 64, kSY = 128, kSD = 16, kSP = kSD + 4;
+
+template <bool BAND>
+__global__ __launch_bounds__(256) void att_dims_kernel(float *__restrict__ S, uint32_t Ts,
+                                                       const float *__restrict__ xf, const float *__restrict__ yf,
+                                                       const float *__restrict__ bias, uint32_t T, uint32_t D,
+                                                       uint32_t dk) {
+    __shared__ __attribute__((aligned(16))) float sa[2][kSQ][kSP], sb[2][kSY][kSP];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wq = w & 1, wy = w >> 1;
+    const uint32_t h = blockIdx.z, i0 = blockIdx.y * kSQ;
+    const uint32_t R = BAND ? 2 * T - 1 : T;
+    const int64_t y0 = BAND ? (int64_t)T - 1 - (int64_t)(i0 + kSQ - 1) + (int64_t)blockIdx.x * kSY
+                            : (int64_t)blockIdx.x * kSY;
+    if (BAND && y0 > (int64_t)(2 * T - 2) - (int64_t)i0)
+        return;                                         /* the whole workgroup: no row meets a key */
+    const uint32_t col = h * dk;
+    /* staging: x row tid % 64, dimensions 4 (tid / 64); y row tid % 128,
+     * dimensions 4 (tid / 128 + 2 k), k < 2 */
+    const int xrw = tid & 63, yrw = tid & 127;
+    const uint32_t xi = min(i0 + xrw, T - 1);
+    const int64_t yl = y0 + yrw;
+    const uint32_t yi = (uint32_t)(yl < 0 ? 0 : yl >= (int64_t)R ? R - 1 : yl);
+    const float *xr = xf + (size_t)xi * D + col, *yr = yf + (size_t)yi * D + col, *br = bias + col;
+    /* a stage's loads, two sets in registers: stage s + 2 is loaded while
+     * stage s is multiplied, so each load has two stages to land */
+    struct Regs {
+        float4 x, b, y[2];
+    };
+    const uint32_t ns = dk / kSD, last = (ns - 1) * kSD;
+    auto load = [&](Regs &g, uint32_t d0) {
+        d0 = d0 < last ? d0 : last;                 /* past the end: the last again, in bounds */
+        g.x = *(const float4 *)(xr + d0 + 4 * (tid >> 6));
+        g.b = *(const float4 *)(br + d0 + 4 * (tid >> 6));
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            g.y[k] = *(const float4 *)(yr + d0 + 4 * ((tid >> 7) + 2 * k));
+    };
+    auto store = [&](const Regs &g, int b) {
+        *(float4 *)&sa[b][xrw][4 * (tid >> 6)] = make_float4(g.x.x + g.b.x, g.x.y + g.b.y, g.x.z + g.b.z,
+                                                             g.x.w + g.b.w);
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            *(float4 *)&sb[b][yrw][4 * ((tid >> 7) + 2 * k)] = g.y[k];
+    };
+    v32f acc;
+#pragma unroll
+    for (int r = 0; r < 32; r++)
+        acc[r] = 0.0f;
+    const int ac = 32 * wq + (lane & 31), bc = 64 * wy + lane;
+    auto mult = [&](int b) {
+        float4 a4[kSD / 4], b4[kSD / 4];
+#pragma unroll
+        for (int k = 0; k < kSD / 4; k++) {
+            a4[k] = *(const float4 *)&sa[b][ac][4 * k];
+            b4[k] = *(const float4 *)&sb[b][bc][4 * k];
+        }
+#pragma unroll
+        for (int k = 0; k < kSD / 4; k++) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a4[k].x, b4[k].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a4[k].y, b4[k].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a4[k].z, b4[k].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a4[k].w, b4[k].w, acc, 0, 0, 0);
+        }
+    };
+    /* ns is even (dk a multiple of 64): stages in pairs, the buffers and
+     * register sets alternating statically */
+    Regs g0, g1;
+    load(g0, 0);
+    load(g1, kSD);
+    store(g0, 0);
+    __syncthreads();
+    for (uint32_t st = 0; st < ns; st += 2) {
+        load(g0, (st + 2) * kSD);
+        mult(0);
+        store(g1, 1);
+        __syncthreads();
+        load(g1, (st + 3) * kSD);
+        mult(1);
+        store(g0, 0);
+        __syncthreads();
+    }
+    if (!BAND) {
+#pragma unroll
+        for (int r = 0; r < 32; r++) {
+            const uint32_t rr = r & 15;
+            const uint32_t qi = i0 + 32 * wq + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+            const int64_t kj = y0 + 64 * wy + 32 * (r >> 4) + (lane & 31);
+            if (qi < T && kj < (int64_t)T)
+                S[((size_t)h * T + qi) * Ts + (uint32_t)kj] = acc[r];
+        }
+    } else {
+        /* a block's 16 old scores first, then their sums: the loads need
+         * not wait on the stores (no two registers hold the same (i, j));
+         * offsets from the head's scores fit 32 bits (the launcher checks) */
+        float *Sh = S + (size_t)h * T * Ts;
+#pragma unroll
+        for (int blk = 0; blk < 2; blk++) {
+            uint32_t at[16];
+            float old[16];
+#pragma unroll
+            for (int rr = 0; rr < 16; rr++) {
+                const uint32_t qi = i0 + 32 * wq + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+                const int64_t kj = y0 + 64 * wy + 32 * blk + (lane & 31) - ((int64_t)T - 1 - (int64_t)qi);
+                const bool in = qi < T && kj >= 0 && kj < (int64_t)T;
+                at[rr] = in ? qi * Ts + (uint32_t)kj : ~0u;
+                old[rr] = in ? Sh[at[rr]] : 0.0f;
+            }
+#pragma unroll
+            for (int rr = 0; rr < 16; rr++)
+                if (at[rr] != ~0u)
+                    Sh[at[rr]] = old[rr] + acc[16 * blk + rr];
+        }
+    }
+}
+
+/* PV: a workgroup 64 queries x 64 dimensions of a head, wave w the queries
+ * i0 + 16 w .. + 15 (16x16x1_4b, its four blocks the 64 dimensions); keys
+ * in stages of 64 through LDS, double-buffered (a stage's loads are in
+ * flight for a stage's 64 MFMAs): the probabilities P = e * (1 / sum)
+ * (formed as staged) query-major and the values dimension-major, each row
+ * of keys contiguous and padded to 68 floats, so that a lane reads four
+ * keys of its query (A) or of its dimension (B) with one 16-byte read, in
+ * distinct banks across the wave; 32 keys' operands are read into
+ * registers before their MFMAs. Exactly the T keys are multiplied. */
+constexpr int kPVK = 64, kPVS = kPVK + 4;
+
+__global__ __launch_bounds__(256) void att_pv_mfma_kernel(float *__restrict__ of, const float *__restrict__ S,
+                                                          const float *__restrict__ inv, uint32_t Ts,
+                                                          const float *__restrict__ vf, uint32_t T, uint32_t D,
+                                                          uint32_t dk) {
+    __shared__ __attribute__((aligned(16))) float sv[2][64][kPVS], sp[2][64][kPVS];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t h = blockIdx.z, d0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
+    const float *Sh = S + (size_t)h * T * Ts;
+    const float *vh = vf + (size_t)h * dk + d0;
+    /* staging: values key tid % 64, dimensions 4 (tid / 64 + 4 k); the
+     * probabilities query tid / 16 + 16 k, keys 4 (tid % 16); k < 4 */
+    const int vk = tid & 63, pr = tid >> 4, pc = 4 * (tid & 15);
+    float rinv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t i = i0 + pr + 16 * k;
+        rinv[k] = i < T ? inv[(size_t)h * T + i] : 0.0f;
+    }
+    float4 rv[4], rp[4];
+    auto load = [&](uint32_t j0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t j = j0 + vk;
+            rv[k] = j < T ? *(const float4 *)(vh + (size_t)j * D + 4 * ((tid >> 6) + 4 * k))
+                          : make_float4(0, 0, 0, 0);
+            const uint32_t i = i0 + pr + 16 * k, jc = j0 + pc;
+            rp[k] = i < T && jc < Ts ? *(const float4 *)(Sh + (size_t)i * Ts + jc) : make_float4(0, 0, 0, 0);
+        }
+    };
+    auto store = [&](int b) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int d = 4 * ((tid >> 6) + 4 * k);
+            sv[b][d][vk] = rv[k].x;
+            sv[b][d + 1][vk] = rv[k].y;
+            sv[b][d + 2][vk] = rv[k].z;
+            sv[b][d + 3][vk] = rv[k].w;
+            const float4 e = rp[k];
+            const float r = rinv[k];
+            *(float4 *)&sp[b][pr + 16 * k][pc] = make_float4(e.x * r, e.y * r, e.z * r, e.w * r);
+        }
+    };
+    v16f acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++)
+        acc[r] = 0.0f;
+    const int arow = 16 * w + (lane & 15);
+    load(0);
+    store(0);
+    __syncthreads();
+    const uint32_t ns = (T + kPVK - 1) / kPVK;
+    for (uint32_t st = 0; st < ns; st++) {
+        const int b = st & 1;
+        const uint32_t j0 = st * kPVK;
+        if (st + 1 < ns)
+            load(j0 + kPVK);
+        if (T - j0 >= (uint32_t)kPVK) {
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                float4 a4[8], b4[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    a4[k] = *(const float4 *)&sp[b][arow][32 * half + 4 * k];
+                    b4[k] = *(const float4 *)&sv[b][lane][32 * half + 4 * k];
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a4[k].x, b4[k].x, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a4[k].y, b4[k].y, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a4[k].z, b4[k].z, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a4[k].w, b4[k].w, acc, 0, 0, 0);
+                }
+            }
+        } else {
+            /* exactly the T keys: a padding step would turn a -0 sum into +0 */
+            const int nk = (int)(T - j0);
+            for (int c = 0; c < nk; c++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x1f32(sp[b][arow][c], sv[b][lane][c], acc, 0, 0, 0);
+        }
+        if (st + 1 < ns)
+            store(b ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const uint32_t qi = i0 + 16 * w + 4 * (lane >> 4) + (r & 3);
+        if (qi < T)
+            of[(size_t)qi * D + h * dk + d0 + 16 * (r >> 2) + (lane & 15)] = acc[r];
+    }
+}
+
 /* --------------------------------------------------------------- dwq --
  *
  * core/encoder.c:158-176 (glu_item, dw_item): h = GLU(u) (backend/ref/
@@ -516,6 +768,16 @@ int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+/* The attention's kernels: 0 the matrix cores' (the default), 1 the VALU
+ * chains; both compute the same bits. */
+static int g_att_valu = 0;
+
+int set_attention_kernels(int valu) {
+    const int was = g_att_valu;
+    g_att_valu = valu ? 1 : 0;
+    return was;
+}
+
 uint32_t att_score_stride(uint32_t T) { return (T + 3) & ~3u; }
 
 size_t att_workspace_floats(uint32_t T, uint32_t H) {
@@ -528,14 +790,23 @@ int launch_attention(float *of, float *ws, const float *qf, const float *kf, con
                      const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s) {
     if (T == 0)
         return 0;
-    if (H == 0 || D % H || (D / H) % 64)
+    if (H == 0 || D % H || (D / H) % 64 || (uint64_t)T * att_score_stride(T) >= (1ull << 32) - 1)
         return -2;
     const uint32_t dk = D / H, Ts = att_score_stride(T), tiles = (T + kAT - 1) / kAT, rows = H * T;
     float *S = ws, *inv = ws + (size_t)rows * Ts;
-    att_scores_kernel<<<dim3(tiles, tiles, H), 256, 0, s>>>(S, Ts, qf, kf, pf, bu, bv, T, D, dk);
+    if (g_att_valu) {
+        att_scores_kernel<<<dim3(tiles, tiles, H), 256, 0, s>>>(S, Ts, qf, kf, pf, bu, bv, T, D, dk);
+    } else {
+        const uint32_t qt = (T + kSQ - 1) / kSQ;
+        att_dims_kernel<false><<<dim3((T + kSY - 1) / kSY, qt, H), 256, 0, s>>>(S, Ts, qf, kf, bu, T, D, dk);
+        att_dims_kernel<true><<<dim3((T + kSQ - 1 + kSY - 1) / kSY, qt, H), 256, 0, s>>>(S, Ts, qf, pf, bv, T, D, dk);
+    }
     const float scale = 1.0f / sqrtf((float)dk);
     att_softmax_kernel<<<(rows + 15) / 16, 256, 0, s>>>(S, inv, Ts, rows, T, scale);
-    att_pv_kernel<<<dim3(dk / kPD, (T + kPI - 1) / kPI, H), 128, 0, s>>>(of, S, inv, Ts, vf, T, D, dk);
+    if (g_att_valu)
+        att_pv_kernel<<<dim3(dk / kPD, (T + kPI - 1) / kPI, H), 128, 0, s>>>(of, S, inv, Ts, vf, T, D, dk);
+    else
+        att_pv_mfma_kernel<<<dim3((T + 63) / 64, dk / 64, H), 256, 0, s>>>(of, S, inv, Ts, vf, T, D, dk);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

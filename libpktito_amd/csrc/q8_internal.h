@@ -84,9 +84,14 @@ int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size
 int ring_count();
 int set_ring(int i);
 
-/* The packed quantize's kernel: 0 one wave a column, 1 one workgroup a
- * group, -1 by size; returns the one forced before. */
+/* The packed quantize's kernel: 0 one wave a column (a wave a 1024-input
+ * chunk of a wide column in blocks), 1 one workgroup a group, 2 one wave a
+ * whole column, -1 by size; returns the one forced before. */
 int set_quant_kernel(int kind);
+
+/* The attention's score and PV kernels: 0 the matrix cores', 1 the VALU
+ * chains; returns the one set before. */
+int set_attention_kernels(int valu);
 
 /* The quantize's op on its inputs (launch_quantize_packed's op). */
 constexpr int kOpPlain = 0, kOpSilu = 1;

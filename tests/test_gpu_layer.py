@@ -129,12 +129,15 @@ def test_dwq(hip, torch, T, D, K, qb):
     check_packed(qp, dt, q, d, D, T)
 
 
-@pytest.mark.parametrize("T,D,H", [(1, 128, 2), (2, 128, 2), (17, 128, 2), (64, 128, 2), (65, 256, 2),
-                                   (130, 128, 2), (100, 1024, 8)])
-def test_attention(hip, torch, T, D, H):
+@pytest.mark.parametrize("valu", [0, 1])
+@pytest.mark.parametrize("T,D,H", [(1, 128, 2), (2, 128, 2), (7, 64, 1), (17, 128, 2), (64, 128, 2), (65, 256, 2),
+                                   (130, 128, 2), (100, 1024, 8), (289, 128, 1)])
+def test_attention(hip, torch, T, D, H, valu):
     """The attention's scores (with the positions' diagonals), softmax and
     weighted values against pk_k_gemm_f32 and pk_k_softmax composed on the
-    CPU with the reference's panel layouts."""
+    CPU with the reference's panel layouts; on the matrix cores (one-step
+    MFMAs) and as VALU chains. T covers one key, partial tiles and bands,
+    and key counts that are not multiples of 8."""
     g = synth.rng(T * 7 + D)
     q, k, v = (g.standard_normal((3, T, D)) * 1.5).astype(np.float32)
     p = g.standard_normal((2 * T - 1, D)).astype(np.float32)
@@ -142,10 +145,14 @@ def test_attention(hip, torch, T, D, H):
     want = attention(q, k, v, p, bu, bv, H)
     o = torch.full((T, D), 9.0, dtype=torch.float32, device="cuda")
     ws = torch.empty((hip.attention_workspace(T, H),), dtype=torch.uint8, device="cuda")
-    say("attention", T, D, H)
-    hip.attention_dev(o, dev(torch, q), dev(torch, k), dev(torch, v), dev(torch, p), dev(torch, bu), dev(torch, bv),
-                      T, D, H, ws)
-    torch.cuda.synchronize()
+    say("attention", T, D, H, valu)
+    was = hip.force_attention(valu)
+    try:
+        hip.attention_dev(o, dev(torch, q), dev(torch, k), dev(torch, v), dev(torch, p), dev(torch, bu),
+                          dev(torch, bv), T, D, H, ws)
+        torch.cuda.synchronize()
+    finally:
+        hip.force_attention(was)
     assert np.array_equal(bits(o.cpu().numpy()), bits(want))
 
 
