@@ -414,8 +414,9 @@ __global__ __launch_bounds__(128) void att_pv_kernel(float *__restrict__ of, con
  * The same chains on the matrix cores: v_mfma_f32_32x32x1_2b_f32 and
  * v_mfma_f32_16x16x1_4b_f32 have one input step (K = 1), so each output
  * takes exactly one product and one add a step, d = fma(a, b, d) with one
- * rounding (checked against v_fma_f32 on 1.2M outputs of every class of
- * input: subnormals, both zeros, infinities, NaN, exact cancellation). A
+ * rounding (measured equal to v_fma_f32 on 1.2M outputs of every class of
+ * input: subnormals, both zeros, infinities, NaN, exact cancellation; the
+ * attention tests compare both paths with the oracle on such operands). A
  * chain of steps in the reference's order is then the reference's fmaf
  * chain, at the matrix cores' rate and with each operand one register a
  * lane for 2048 (or 1024) chains.

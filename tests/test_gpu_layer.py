@@ -156,6 +156,46 @@ def test_attention(hip, torch, T, D, H, valu):
     assert np.array_equal(bits(o.cpu().numpy()), bits(want))
 
 
+@pytest.mark.parametrize("valu", [0, 1])
+def test_attention_special_values(hip, torch, valu):
+    """Subnormal and signed-zero operands, products past the float range and
+    NaNs in the queries, keys, values and positions: every chain step's one
+    rounding (an MFMA step or a v_fma_f32) gives the oracle's bits, NaNs
+    compared as NaN."""
+    T, D, H = 37, 128, 2
+    g = synth.rng(4242)
+    q, k, v = (g.standard_normal((3, T, D)) * 1.5).astype(np.float32)
+    p = g.standard_normal((2 * T - 1, D)).astype(np.float32)
+    bu, bv = (0.3 * g.standard_normal((2, D))).astype(np.float32)
+    tiny = np.float32(1e-41)
+    q[3, :] = tiny * np.sign(q[3, :])          # subnormal queries: their products underflow
+    k[5, ::3] = -0.0
+    k[6, :] = tiny
+    v[7, :] = np.float32(-1e-40)
+    v[8, 10] = np.inf                          # P * inf through PV's chain
+    v[13, 20] = np.nan
+    q[9, 0] = np.float32(3e30)                 # a score past the float range
+    k[9, 0] = np.float32(3e30)
+    p[20, 4] = np.float32(2e38)
+    q[11, 4] = np.float32(1e10)
+    k[12, 7] = np.nan                          # a NaN score: the softmax's exp clamps it
+    bu[1] = -0.0
+    bv[2] = tiny
+    want = attention(q, k, v, p, bu, bv, H)
+    o = torch.full((T, D), 9.0, dtype=torch.float32, device="cuda")
+    ws = torch.empty((hip.attention_workspace(T, H),), dtype=torch.uint8, device="cuda")
+    say("attention special values", valu)
+    was = hip.force_attention(valu)
+    try:
+        hip.attention_dev(o, dev(torch, q), dev(torch, k), dev(torch, v), dev(torch, p), dev(torch, bu),
+                          dev(torch, bv), T, D, H, ws)
+        torch.cuda.synchronize()
+    finally:
+        hip.force_attention(was)
+    assert np.isnan(want).any() and np.isinf(want).any() and np.isfinite(want).any()
+    assert np.array_equal(bits(o.cpu().numpy()), bits(want))
+
+
 def run_layer(hip, torch, D, H, F, K, T, qb, seed, threads=16):
     g = synth.rng(seed)
     w = layer_weights(g, D=D, H=H, F=F, K=K)
