@@ -616,8 +616,8 @@ def main():
     host_inputs = [(p.x_host.reshape(-1), p.w, p.ws, p.M, p.K, p.N, p.add) for p in prods]
     log(f"layer: {ms:.4f} ms a step, {tops:.1f} TOPS; dominant {dom.name} {dkms * 1e3:.2f} us")
     # the real encoder's blocks (qb = 32 by default, 64 in its fast mode): the
-    # same layer with blocked quantizes and products on the packed path (one
-    # launch a product: the batch takes per-row blocks only)
+    # same layer with blocked quantizes and products on the packed path, q, k,
+    # v and pos in one launch as in the per-row step
     blocked = {}
     for qb in (32, 64):
         bd = {p.name: torch.empty((p.M * p.K // qb,), dtype=torch.float32, device=p.x.device) for p in prods}
@@ -631,6 +631,12 @@ def main():
                 o = src[owner.get(p.name, p.name)]
                 if p.name not in owner and p.name != "pos":
                     pk.quantize_packed_dev(None, p.qp, bd[p.name], p.x, p.K, p.M, p.xs, qb=qb)
+                if p.name in ATTENTION:
+                    if p.name == ATTENTION[0]:
+                        group = [(a, src[owner.get(a.name, a.name)]) for a in prods if a.name in ATTENTION]
+                        pk.gemm_q8_batch_dev([(a.out, a.N, a.m, 0, a.N, a.m.dev_scales, None, ao.qp, bd[ao.name],
+                                               a.K, a.M, a.add) for a, ao in group], qb=qb)
+                    continue
                 pk.gemm_q8_packed_dev(p.out, p.N, p.m, 0, p.N, p.m.dev_scales, None, o.qp, bd[o.name], p.K, p.M,
                                       p.add, qb=qb)
         gb = graph_of(torch, blocked_step)

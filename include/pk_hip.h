@@ -172,8 +172,8 @@ int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, c
                                void *stream);
 
 /* One product of a batch: an uploaded matrix's run of panels [r0, r0 + rows)
- * with its scales and bias at r0 (device), the packed per-row activations qp
- * of a (a->q is not read), and the outputs out[t * os + r]. */
+ * with its scales and bias at r0 (device), the packed activations qp of a
+ * (a->q is not read), and the outputs out[t * os + r]. */
 typedef struct {
     float             *out;
     size_t             os;
@@ -189,8 +189,8 @@ typedef struct {
  * pk_hip_gemm_q8_packed_dev gives it alone. The reference runs such products
  * one after another (core/encoder.c:329-368: the attention's q, k and v of one
  * activation, and the positions' projection); a device-resident caller
- * launches them together. The jobs share n and per-row blocks (qb == n);
- * device pointers throughout. */
+ * launches them together. The jobs share n and qb (per-row, qb == n, or
+ * blocks of 32 or 64); device pointers throughout. */
 int pk_hip_gemm_q8_batch_dev(const pk_hip_job *jobs, uint32_t njobs, int rmode, void *stream);
 
 /* ----------------------------------------- the device-resident layer --- */

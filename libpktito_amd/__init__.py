@@ -322,14 +322,14 @@ def gemm_q8_grouped_dev(m, r0, rows, ws_ptr, bias, segs, add, stream=None):
                                             int(add), _stream(stream)))
 
 
-def gemm_q8_batch_dev(jobs, rmode=0, stream=None):
+def gemm_q8_batch_dev(jobs, rmode=0, stream=None, qb=None):
     """Independent products in one launch: jobs [(out, os, m, r0, rows, ws_ptr,
     bias, qp, d, n, T, add), ...] of device tensors, m a Q8Matrix, qp packed
-    per-row activations."""
+    activations in blocks of qb (default: per-row, qb = n)."""
     arr = (Job * len(jobs))()
     for i, (out, os_, m, r0, rows, ws_ptr, bias, qp, d, n, T, add) in enumerate(jobs):
-        arr[i] = Job(_dptr(out), os_, m.handle, r0, rows, ws_ptr, _dptr(bias), Act(None, _dptr(d), n, n, T),
-                     _dptr(qp), int(add))
+        arr[i] = Job(_dptr(out), os_, m.handle, r0, rows, ws_ptr, _dptr(bias),
+                     Act(None, _dptr(d), n, n if qb is None else qb, T), _dptr(qp), int(add))
     _check(lib().pk_hip_gemm_q8_batch_dev(arr, len(jobs), int(rmode), _stream(stream)))
 
 

@@ -664,15 +664,16 @@ int pk_hip_gemm_q8_batch_dev(const pk_hip_job *jobs, uint32_t njobs, int rmode, 
         return fail(PK_HIP_EROUND, "gemm_q8_batch_dev: rmode %d", rmode);
     pkq8::JobTable tab;
     tab.njobs = njobs;
-    const uint32_t n = jobs[0].a.n;
+    const uint32_t n = jobs[0].a.n, qb = jobs[0].a.qb;
     for (uint32_t j = 0; j < njobs; j++) {
         const pk_hip_job &jb = jobs[j];
         const pk_hip_act *a = &jb.a;
         if (!jb.m)
             return fail(PK_HIP_ENOTUP, "gemm_q8_batch_dev: job %u has no matrix", j);
-        if (a->n != n || a->qb != n || n % 32 || n > 16384)
-            return fail(PK_HIP_EINVAL, "gemm_q8_batch_dev: job %u has n %u qb %u; the jobs share n and qb == n",
-                        j, a->n, a->qb);
+        if (a->n != n || a->qb != qb || !(qb == n || qb == 32 || qb == 64) || n % qb || n % 32 || n > 16384)
+            return fail(PK_HIP_EINVAL,
+                        "gemm_q8_batch_dev: job %u has n %u qb %u; the jobs share n and qb (n, 32 or 64)", j,
+                        a->n, a->qb);
         if (a->T && (!a->d || !jb.qp || ((uintptr_t)jb.qp & 15) || !jb.out || !jb.ws))
             return fail(PK_HIP_EINVAL, "gemm_q8_batch_dev: job %u needs out, ws, d and a 16-byte aligned qp", j);
         if (a->T > 1 && jb.os < jb.rows)
@@ -691,8 +692,8 @@ int pk_hip_gemm_q8_batch_dev(const pk_hip_job *jobs, uint32_t njobs, int rmode, 
         g.n = n;
         g.ku = jb.m->ku;
         g.kr = pkq8::units_with_data(jb.m->cols);
-        g.qb = n;
-        g.nb = 1;
+        g.qb = qb;
+        g.nb = n / qb;
         g.add = jb.add;
         g.rmode = rmode;
         tab.s[j] = pkq8::Seg{ jb.out, jb.qp, a->d, (uint64_t)jb.os,
@@ -971,9 +972,18 @@ int pk_hip_layer_dev(const pk_hip_layer *L, float *x, uint32_t T, const int8_t *
     /* the attention (core/encoder.c:339-352) */
     PK_LAUNCH(pkq8::launch_normq(w.act_qp, w.act_d, x, D, T, L->att_nw, L->att_nb, L->eps, qb, s),
               "layer normq launch");
-    if ((e = gemm(w.qf, D, L->q, &act, w.act_qp, 0)) || (e = gemm(w.kf, D, L->k, &act, w.act_qp, 0)) ||
-        (e = gemm(w.vf, D, L->v, &act, w.act_qp, 0)) || (e = gemm(w.pf, D, L->pos, &ape, ape_qp, 0)))
-        return e;
+    {
+        /* q, k and v of one activation and the positions' projection: one
+         * launch (independent products, each its bits alone) */
+        const pk_hip_job jobs[4] = {
+            { w.qf, D, L->q, 0, D, L->q->s, nullptr, act, w.act_qp, 0 },
+            { w.kf, D, L->k, 0, D, L->k->s, nullptr, act, w.act_qp, 0 },
+            { w.vf, D, L->v, 0, D, L->v->s, nullptr, act, w.act_qp, 0 },
+            { w.pf, D, L->pos, 0, D, L->pos->s, nullptr, ape, ape_qp, 0 },
+        };
+        if ((e = pk_hip_gemm_q8_batch_dev(jobs, 4, 0, stream)))
+            return e;
+    }
     PK_LAUNCH(pkq8::launch_attention(w.of, w.S, w.qf, w.kf, w.vf, w.pf, L->bias_u, L->bias_v, T, D, L->H, s),
               "layer attention launch");
     PK_LAUNCH(pkq8::launch_quantize_packed(nullptr, w.act_qp, w.act_d, w.of, D, D, qb, T, s, &name),

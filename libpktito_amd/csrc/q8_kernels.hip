@@ -1528,7 +1528,7 @@ static void run_pipe1(const GemmArgs &g, const SegTable &tab, hipStream_t s) {
     }
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG>
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, int BLK>
 __global__ __launch_bounds__(64 * WN * WM * KG) void gemm_pipe_batch_kernel(JobTable tab) {
     uint32_t j = 0;
     while (j + 1 < tab.njobs && tab.wg0[j + 1] <= blockIdx.x)
@@ -1539,10 +1539,10 @@ __global__ __launch_bounds__(64 * WN * WM * KG) void gemm_pipe_batch_kernel(JobT
     const uint32_t tiles_n = tab.tiles_n[j];
     uint32_t tn, tm;
     xcd_tile(b, tab.tiles[j], tiles_n, tab.tiles[j] / tiles_n, tn, tm);
-    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, true, 0>(tab.g[j], tab.s[j], tn, tm);
+    pipe_tile<WN, WM, TN, TM, UPS, NS, KG, true, BLK>(tab.g[j], tab.s[j], tn, tm);
 }
 
-template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG>
+template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG, int BLK = 0>
 static void run_pipe_batch(const JobTable &jobs, hipStream_t s) {
     constexpr uint32_t BN = 16 * TN * WN, BM = 16 * TM * WM;
     JobTable t = jobs;
@@ -1554,7 +1554,7 @@ static void run_pipe_batch(const JobTable &jobs, hipStream_t s) {
         wg += (t.tiles[j] + 7) / 8 * 8;
     }
     t.wg0[t.njobs] = wg;
-    gemm_pipe_batch_kernel<WN, WM, TN, TM, UPS, NS, KG><<<wg, 64 * WN * WM * KG, 0, s>>>(t);
+    gemm_pipe_batch_kernel<WN, WM, TN, TM, UPS, NS, KG, BLK><<<wg, 64 * WN * WM * KG, 0, s>>>(t);
 }
 
 template <int WN, int WM, int TN, int TM, int UPS, int NS, int KG = 1, int BLK = 0>
@@ -1576,6 +1576,8 @@ struct RingCfg {
     void (*batch)(const JobTable &, hipStream_t);   /* pipe_tile only */
     void (*run64)(const GemmArgs &, const SegTable &, hipStream_t);   /* blocks of 64 inputs, or null */
     void (*run32)(const GemmArgs &, const SegTable &, hipStream_t);   /* blocks of 32 inputs, or null */
+    void (*batch64)(const JobTable &, hipStream_t);                   /* batches in blocks of 64, or null */
+    void (*batch32)(const JobTable &, hipStream_t);                   /* batches in blocks of 32, or null */
 };
 static const RingCfg kRing[] = {
     /* ring_tile: name <channels x frames, units a stage> */
@@ -1585,9 +1587,9 @@ static const RingCfg kRing[] = {
     { "ring<64x64,4>", 64, 64, 4, 0, 1, run_ring<2, 2, 2, 2, 4>, nullptr, nullptr, nullptr },
     /* pipe_tile: name <channels x frames, units a stage, slots>; w8: eight
      * waves of 64 x 32 */
-    { "pipe<128x128,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 2, 4, 4, 1, 4, 1>, run_pipe_batch<2, 2, 4, 4, 1, 4, 1>, run_pipe<2, 2, 4, 4, 1, 4, 1, 1>, run_pipe<2, 2, 4, 4, 1, 4, 1, 2> },
-    { "pipe<128x128w8,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 4, 4, 2, 1, 4, 1>, run_pipe_batch<2, 4, 4, 2, 1, 4, 1>, run_pipe<2, 4, 4, 2, 1, 4, 1, 1>, run_pipe<2, 4, 4, 2, 1, 4, 1, 2> },
-    { "pipe<64x64,2,4>", 64, 64, 2, 4, 1, run_pipe<2, 2, 2, 2, 2, 4, 1>, run_pipe_batch<2, 2, 2, 2, 2, 4, 1>, run_pipe<2, 2, 2, 2, 2, 4, 1, 1>, run_pipe<2, 2, 2, 2, 2, 4, 1, 2> },
+    { "pipe<128x128,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 2, 4, 4, 1, 4, 1>, run_pipe_batch<2, 2, 4, 4, 1, 4, 1>, run_pipe<2, 2, 4, 4, 1, 4, 1, 1>, run_pipe<2, 2, 4, 4, 1, 4, 1, 2>, run_pipe_batch<2, 2, 4, 4, 1, 4, 1, 1>, run_pipe_batch<2, 2, 4, 4, 1, 4, 1, 2> },
+    { "pipe<128x128w8,1,4>", 128, 128, 1, 4, 1, run_pipe<2, 4, 4, 2, 1, 4, 1>, run_pipe_batch<2, 4, 4, 2, 1, 4, 1>, run_pipe<2, 4, 4, 2, 1, 4, 1, 1>, run_pipe<2, 4, 4, 2, 1, 4, 1, 2>, run_pipe_batch<2, 4, 4, 2, 1, 4, 1, 1>, run_pipe_batch<2, 4, 4, 2, 1, 4, 1, 2> },
+    { "pipe<64x64,2,4>", 64, 64, 2, 4, 1, run_pipe<2, 2, 2, 2, 2, 4, 1>, run_pipe_batch<2, 2, 2, 2, 2, 4, 1>, run_pipe<2, 2, 2, 2, 2, 4, 1, 1>, run_pipe<2, 2, 2, 2, 2, 4, 1, 2>, run_pipe_batch<2, 2, 2, 2, 2, 4, 1, 1>, run_pipe_batch<2, 2, 2, 2, 2, 4, 1, 2> },
     { "pipe<64x64,4,4>", 64, 64, 4, 4, 1, run_pipe<2, 2, 2, 2, 4, 4, 1>, run_pipe_batch<2, 2, 2, 2, 4, 4, 1>, nullptr, nullptr },
     /* eight waves of 64 x 64 */
     { "pipe<128x256w8,1,4>", 128, 256, 1, 4, 1, run_pipe<2, 4, 4, 4, 1, 4, 1>, run_pipe_batch<2, 4, 4, 4, 1, 4, 1>, nullptr, nullptr },
@@ -1600,12 +1602,12 @@ static const RingCfg kRing[] = {
     { "pipe<64x64,1,4,k2>", 64, 64, 1, 4, 2, run_pipe<2, 2, 2, 2, 1, 4, 2>, run_pipe_batch<2, 2, 2, 2, 1, 4, 2>, nullptr, nullptr },
     { "pipe<64x64,2,2,k2>", 64, 64, 2, 2, 2, run_pipe<2, 2, 2, 2, 2, 2, 2>, run_pipe_batch<2, 2, 2, 2, 2, 2, 2>, nullptr, nullptr },
     /* three slots: three workgroups a CU */
-    { "pipe<64x64,2,3>", 64, 64, 2, 3, 1, run_pipe<2, 2, 2, 2, 2, 3, 1>, run_pipe_batch<2, 2, 2, 2, 2, 3, 1>, run_pipe<2, 2, 2, 2, 2, 3, 1, 1>, run_pipe<2, 2, 2, 2, 2, 3, 1, 2> },
+    { "pipe<64x64,2,3>", 64, 64, 2, 3, 1, run_pipe<2, 2, 2, 2, 2, 3, 1>, run_pipe_batch<2, 2, 2, 2, 2, 3, 1>, run_pipe<2, 2, 2, 2, 2, 3, 1, 1>, run_pipe<2, 2, 2, 2, 2, 3, 1, 2>, run_pipe_batch<2, 2, 2, 2, 2, 3, 1, 1>, run_pipe_batch<2, 2, 2, 2, 2, 3, 1, 2> },
     { "pipe<64x64,2,3,k2>", 64, 64, 2, 3, 2, run_pipe<2, 2, 2, 2, 2, 3, 2>, run_pipe_batch<2, 2, 2, 2, 2, 3, 2>, nullptr, nullptr },
     /* eight waves of 32 x 16: two a SIMD, so one wave's block chain runs
      * beside the other's MFMAs where a product has too few tiles for two
      * workgroups a CU */
-    { "pipe<64x64w8,2,4>", 64, 64, 2, 4, 1, run_pipe<2, 4, 2, 1, 2, 4, 1>, run_pipe_batch<2, 4, 2, 1, 2, 4, 1>, run_pipe<2, 4, 2, 1, 2, 4, 1, 1>, run_pipe<2, 4, 2, 1, 2, 4, 1, 2> },
+    { "pipe<64x64w8,2,4>", 64, 64, 2, 4, 1, run_pipe<2, 4, 2, 1, 2, 4, 1>, run_pipe_batch<2, 4, 2, 1, 2, 4, 1>, run_pipe<2, 4, 2, 1, 2, 4, 1, 1>, run_pipe<2, 4, 2, 1, 2, 4, 1, 2>, run_pipe_batch<2, 4, 2, 1, 2, 4, 1, 1>, run_pipe_batch<2, 4, 2, 1, 2, 4, 1, 2> },
 };
 constexpr int kNRing = sizeof kRing / sizeof kRing[0];
 
@@ -1785,11 +1787,18 @@ int launch_gemm_batch(const JobTable &jobs, hipStream_t s, const char **name) {
     }
     if (jobs.njobs == 0 || frames == 0)
         return 0;
-    /* the tiling the jobs would take as one product of their frames */
-    const int c = pick_ring(rows, frames, jobs.g[0].ku);
-    if (kRing[c].batch) {
-        kRing[c].batch(jobs, s);
-        *name = kRing[c].name;
+    /* the tiling the jobs would take as one product of their frames; every
+     * job shares the blocks (the caller checks) */
+    const GemmArgs &g0 = jobs.g[0];
+    const int mode = g0.qb == g0.n ? 0 : g0.qb == 64 ? 1 : g0.qb == 32 ? 2 : -1;
+    const int c = mode == 0 ? pick_ring(rows, frames, g0.ku) : pick_blocked(rows, frames, g0.ku);
+    auto batch = mode == 0 ? kRing[c].batch : mode == 1 ? kRing[c].batch64 : mode == 2 ? kRing[c].batch32 : nullptr;
+    if (batch) {
+        batch(jobs, s);
+        static thread_local char buf[96];
+        static const char *const modes[] = { "", " blocks of 64k", " blocks of 32k" };
+        snprintf(buf, sizeof buf, "%s%s", kRing[c].name, modes[mode]);
+        *name = buf;
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     /* inputs too short for the pipelined tile: one launch a job */

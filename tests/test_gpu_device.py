@@ -198,13 +198,16 @@ def test_packed_path(hip, torch, M, K, N):
             hip.force_tiling(-1)
 
 
+@pytest.mark.parametrize("qb", [None, 32, 64])
 @pytest.mark.parametrize("K", [1024, 4096, 128])
-def test_batch_of_products(hip, torch, K):
+def test_batch_of_products(hip, torch, K, qb):
     """Independent products in one launch (the attention's q, k, v and the
     positions' projection at once): each job's outputs are the bits its own
     launch gives, with jobs of different frame counts, channel counts, a run
-    of interior panels, bias and add; under the heuristic and under every
-    tiling (short inputs fall back to one launch a job)."""
+    of interior panels, bias and add, per-row or in blocks of 32 or 64; under
+    the heuristic and under every tiling (short inputs, and tilings without
+    a blocked batch, fall back to one launch a job)."""
+    nb = 1 if qb is None else K // qb
     dev = torch.device("cuda")
     g = synth.rng(K + 17)
     specs = [(37, 1024, 0, 1024, False, 0), (750, 1024, 0, 1024, True, 1), (1, 512, 0, 512, False, 0),
@@ -217,9 +220,9 @@ def test_batch_of_products(hip, torch, K):
         mats.append(m)
         x = torch.from_numpy(synth.activations(g, max(T, 1), K)).to(dev)
         qp = torch.zeros((hip.packed_bytes(K, max(T, 1)),), dtype=torch.int8, device=dev)
-        d = torch.empty((max(T, 1),), dtype=torch.float32, device=dev)
+        d = torch.empty((max(T, 1) * nb,), dtype=torch.float32, device=dev)
         if T:
-            hip.quantize_packed_dev(None, qp, d, x, K, T, K)
+            hip.quantize_packed_dev(None, qp, d, x, K, T, K, qb=K if qb is None else qb)
         bias = torch.from_numpy(g.standard_normal(N).astype(np.float32)).to(dev) if use_bias else None
         os_ = N + 3
         base = torch.from_numpy(g.standard_normal(max(T, 1) * os_).astype(np.float32)).to(dev)
@@ -232,7 +235,7 @@ def test_batch_of_products(hip, torch, K):
         out = base.clone()
         if T:
             hip.gemm_q8_packed_dev(None, os_, m, r0, rows, ws_ptr, bias_v, qp, d, K, T, add,
-                                   out_ptr=out.data_ptr() + 4 * r0)
+                                   out_ptr=out.data_ptr() + 4 * r0, qb=K if qb is None else qb)
         want.append(out)
     torch.cuda.synchronize()
     try:
@@ -242,8 +245,8 @@ def test_batch_of_products(hip, torch, K):
             jobs = []
             for o, (base, os_, m, r0, rows, ws_ptr, bias_v, qp, d, T, add) in zip(outs, singles):
                 jobs.append((o[r0:], os_, m, r0, rows, ws_ptr, bias_v, qp, d, K, T, add))
-            say("batch", K, ti)
-            hip.gemm_q8_batch_dev(jobs)
+            say("batch", K, qb, ti)
+            hip.gemm_q8_batch_dev(jobs, qb=qb)
             torch.cuda.synchronize()
             for j, (o, wnt) in enumerate(zip(outs, want)):
                 assert np.array_equal(bits(o.cpu().numpy()), bits(wnt.cpu().numpy())), (ti, j, hip.last_kernel())
