@@ -321,6 +321,42 @@ int launch_quant(pk_hip_act *a, const float *x, size_t xs, hipStream_t s) {
     return PK_HIP_OK;
 }
 
+/* The whole of matrix m times the packed activations qp of a, the outputs
+ * SiLU'd and quantized in blocks of oqb into the packed copy oqp and od (the
+ * up product and siluq of core/encoder.c:130-156 in one launch). Returns 0
+ * launched, 1 where the tiling has no such epilogue (nothing launched), or
+ * minus an error code. */
+int launch_product_siluq(const pk_hip_q8 *m, const pk_hip_act *a, const int8_t *qp, int8_t *oqp, float *od,
+                         uint32_t oqb, hipStream_t s) {
+    pkq8::GemmArgs g;
+    g.w = m->w;
+    g.wstride = (uint64_t)(m->rows / 16) * pkq8::kUnitBytes;
+    g.ws = m->s;
+    g.bias = nullptr;
+    g.rows = m->rows;
+    g.n = a->n;
+    g.ku = m->ku;
+    g.kr = pkq8::units_with_data(m->cols);
+    g.qb = a->qb;
+    g.nb = a->n / a->qb;
+    g.add = 0;
+    g.rmode = 0;
+    g.oqp = oqp;
+    g.od = od;
+    g.oqb = oqb;
+    pkq8::SegTable tab;
+    tab.nseg = 1;
+    tab.s[0] = pkq8::Seg{ nullptr, qp, a->d, 0, (uint64_t)pkq8::packed_groups(a->T) * pkq8::kUnitBytes, a->T, 0 };
+    const char *name = "";
+    const int r = pkq8::launch_gemm(g, tab, s, &name);
+    if (r == -3)
+        return 1;
+    if (r)
+        return -hip_fail(hipGetLastError(), "gemm_q8 silu-quantized launch");
+    g_kernel = name;
+    return 0;
+}
+
 int launch_product(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
                    const float *ws, const float *bias, const pk_hip_act *a, int add, int rmode,
                    hipStream_t s, const int8_t *qp = nullptr) {
@@ -956,15 +992,23 @@ int pk_hip_layer_dev(const pk_hip_layer *L, float *x, uint32_t T, const int8_t *
     auto gemm = [&](float *out, size_t os, const pk_hip_q8 *m, const pk_hip_act *a, const int8_t *qp, int add) {
         return launch_product(out, os, m, 0, m->rows, m->s, nullptr, a, add, 0, s, qp);
     };
-    /* ff (core/encoder.c:321-327): x += down(siluq(up(normq(x)))) */
+    /* ff (core/encoder.c:321-327): x += down(siluq(up(normq(x)))); the SiLU
+     * quantize in the up product's epilogue where its tile has one (the
+     * same bytes and scales: the fp32 hidden activations are never written),
+     * else a pass of its own over them */
     auto ff = [&](const float *nw, const float *nb, const pk_hip_q8 *up, const pk_hip_q8 *down) {
         PK_LAUNCH(pkq8::launch_normq(w.act_qp, w.act_d, x, D, T, nw, nb, L->eps, qb, s), "layer normq launch");
-        int r = gemm(w.u, F, up, &act, w.act_qp, 0);
-        if (r)
-            return r;
-        PK_LAUNCH(pkq8::launch_quantize_packed(nullptr, w.hid_qp, w.hid_d, w.u, F, F, qb, T, s, &name,
-                                               pkq8::kOpSilu),
-                  "layer siluq launch");
+        const int f = launch_product_siluq(up, &act, w.act_qp, w.hid_qp, w.hid_d, qb, s);
+        if (f > 0) {
+            int r = gemm(w.u, F, up, &act, w.act_qp, 0);
+            if (r)
+                return r;
+            PK_LAUNCH(pkq8::launch_quantize_packed(nullptr, w.hid_qp, w.hid_d, w.u, F, F, qb, T, s, &name,
+                                                   pkq8::kOpSilu),
+                      "layer siluq launch");
+        } else if (f < 0) {
+            return -f;
+        }
         return gemm(x, D, down, &hid, w.hid_qp, 1);
     };
     if ((e = ff(L->ff1_nw, L->ff1_nb, L->ff1_up, L->ff1_down)))

@@ -67,6 +67,13 @@ struct GemmArgs {
     uint32_t qb, nb;            /* block inputs, blocks a column */
     int add;
     int rmode;                  /* 0 nearest, 1 upward, 2 downward, 3 toward zero */
+    /* with oqp set (blocked products on 64 x 64 pipelined tiles, all rows of
+     * the matrix, nearest rounding): the outputs are not stored but SiLU'd and
+     * quantized in blocks of oqb into the packed copy oqp and the scales od,
+     * the next product's activations, as a SiLU quantize of them would */
+    int8_t *oqp = nullptr;
+    float *od = nullptr;
+    uint32_t oqb = 0;
 };
 
 int launch_repack(int8_t *dst, const int8_t *src, uint32_t rows, uint32_t cols, hipStream_t s);
@@ -121,7 +128,8 @@ int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstr
                  const float *bias, const float *f, const float *gp, uint32_t rows, uint32_t J, uint32_t kr,
                  uint32_t V, uint32_t n_dur, hipStream_t s);
 
-/* One product; table->nseg == 1 for a plain call. */
+/* One product; table->nseg == 1 for a plain call. With g.oqp set, -3 where
+ * the fused SiLU quantize is not available (nothing launched). */
 int launch_gemm(const GemmArgs &g, const SegTable &table, hipStream_t s, const char **name);
 
 /* Independent products in one launch: job j is the product g[j] x s[j] (one

@@ -1376,6 +1376,82 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
                     acc[i][j] += xch[(((h - 1) * NW + wave) * TN * TM + i * TM + j) * 64 + lane];
     }
 
+    if constexpr (BLK != 0 && WN == 2 && TN == 2) {
+        if (g.oqp) {
+            /* The outputs SiLU'd and quantized in blocks of oqb channels
+             * (core/encoder.c:130-156) straight into the next product's
+             * packed activations: the values are those the store below would
+             * write, and pk_silu, the block's largest magnitude, its scales
+             * and the rounding are the quantizer's own, so the bytes and
+             * scales are a SiLU quantize's of the stored outputs. A wave
+             * holds 32 channels of a frame in 4 lanes (l % 16 the frame) x 8
+             * values: a block of 32 is one wave's, a block of 64 the two
+             * channel waves', met in LDS. */
+            __shared__ int bmax[BM][2];
+            const uint32_t G = (T + 15) / 16;
+            float sv[TM][TN][4];
+            int mx[TM];
+#pragma unroll
+            for (int j = 0; j < TM; j++) {
+                int m = 0;
+#pragma unroll
+                for (int i = 0; i < TN; i++) {
+                    const uint32_t cl = (wn * TN + i) * 16 + (lane >> 4) * 4;
+                    const float4 wsv = *(const float4 *)&epi[ED * 64 + cl];
+                    const float wsr[4] = { wsv.x, wsv.y, wsv.z, wsv.w };
+                    float bsr[4] = { 0, 0, 0, 0 };
+                    if (g.bias) {
+                        const float4 bv = *(const float4 *)&epi[(ED + EW) * 64 + cl];
+                        bsr[0] = bv.x; bsr[1] = bv.y; bsr[2] = bv.z; bsr[3] = bv.w;
+                    }
+                    const float4 af = accf[i][j];
+                    const float a4[4] = { af.x, af.y, af.z, af.w };
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        float v = a4[r] * wsr[r];
+                        if (g.bias)
+                            v = v + bsr[r];
+                        sv[j][i][r] = pk_silu(v);
+                        m = max(m, mag_bits(sv[j][i][r]));
+                    }
+                }
+                m = max(m, __shfl_xor(m, 16));
+                mx[j] = max(m, __shfl_xor(m, 32));
+            }
+            if (g.oqb == 64) {
+#pragma unroll
+                for (int j = 0; j < TM; j++)
+                    if (lane < 16)
+                        bmax[(wm * TM + j) * 16 + lane][wn] = mx[j];
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < TM; j++) {
+                    const int fl = (wm * TM + j) * 16 + (lane & 15);
+                    mx[j] = max(bmax[fl][0], bmax[fl][1]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < TM; j++) {
+                const uint32_t t = m0 + (wm * TM + j) * 16 + (lane & 15);
+                if (t >= T)
+                    continue;
+                bool zero;
+                float dv, id;
+                block_scales((uint32_t)mx[j], zero, dv, id);
+#pragma unroll
+                for (int i = 0; i < TN; i++) {
+                    const uint32_t c = n0 + (wn * TN + i) * 16 + (lane >> 4) * 4;
+                    const int v4 = zero ? 0 : pack4(make_float4(sv[j][i][0], sv[j][i][1], sv[j][i][2], sv[j][i][3]), id);
+                    *(int *)(g.oqp + ((size_t)(c >> 6) * G + (t >> 4)) * kUnitBytes + in_unit(c, t & 15)) = v4;
+                }
+                const uint32_t cb = n0 + wn * 32;       /* the wave's first channel */
+                if ((lane >> 4) == 0 && cb % g.oqb == 0)
+                    g.od[(size_t)t * (g.rows / g.oqb) + cb / g.oqb] = dv;
+            }
+            return;
+        }
+    }
+
     const bool vec = ((sg.os & 3) == 0) && ((((uintptr_t)sg.out) & 15) == 0);
 #pragma unroll
     for (int j = 0; j < TM; j++) {
@@ -1727,6 +1803,8 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
     const int mode = g.qb == g.n ? 0 : g.qb % 64 == 0 ? 1 : 2;
     static const char *const modes[] = { "per-column", "blocks of 64k", "blocks of 32k" };
     static thread_local char buf[96];
+    if (g.oqp && (mode == 0 || g.rmode != 0 || tab.nseg != 1 || !(g.oqb == 32 || g.oqb == 64) || g.rows % 64))
+        return -3;                                  /* no fused SiLU quantize here */
     if (mode == 0 && tab.nseg == 1 && tmax <= 16) {
         const uint32_t panels = g.rows / 16;
         const bool packed = tab.s[0].qstride != 0;
@@ -1757,14 +1835,23 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
         int c = pick_blocked(g.rows, frames, g.ku);
         if (!(mode == 1 ? kRing[c].run64 : kRing[c].run32))
             c = fits(6, g.ku) ? 6 : 4;      /* 4 takes any ku: one unit a stage, four slots */
+        if (g.oqp && (kRing[c].bn != 64 || kRing[c].bm != 64 || kRing[c].slots == 0 || kRing[c].kg != 1)) {
+            /* the fused epilogue is the 64 x 64 pipelined tiles' (two channel
+             * waves of 32) */
+            if (!fits(6, g.ku))
+                return -3;
+            c = 6;
+        }
         auto run = mode == 1 ? kRing[c].run64 : kRing[c].run32;
         if (run) {
             run(g, tab, s);
-            snprintf(buf, sizeof buf, "%s %s", kRing[c].name, modes[mode]);
+            snprintf(buf, sizeof buf, "%s %s%s", kRing[c].name, modes[mode], g.oqp ? " silu-quantized" : "");
             *name = buf;
             return hipGetLastError() == hipSuccess ? 0 : -1;
         }
     }
+    if (g.oqp)
+        return -3;
     /* 128 x 128 tiles where they fill the chip, 64 x 64 where they do not */
     const uint64_t big = (uint64_t)((g.rows + 127) / 128) * ((frames + 127) / 128);
     if (big >= 256) {
