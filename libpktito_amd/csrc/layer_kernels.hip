@@ -316,6 +316,46 @@ __global__ __launch_bounds__(256) void att_softmax_kernel(float *__restrict__ S,
         inv[row] = r;
 }
 
+/* The same for rows of at most 16 REG keys: a lane's keys l, l + 16, ...
+ * loaded at once into registers (one memory round trip a row instead of one
+ * a few keys), the max, then e and the chain from registers in key order. */
+template <int REG>
+__global__ __launch_bounds__(256) void att_softmax_reg_kernel(float *__restrict__ S, float *__restrict__ inv,
+                                                              uint32_t Ts, uint32_t rows, uint32_t T, float scale) {
+    const uint32_t row = blockIdx.x * 16 + (threadIdx.x >> 4), l = threadIdx.x & 15;
+    if (row >= rows)
+        return;
+    float *x = S + (size_t)row * Ts;
+    float v[REG];
+#pragma unroll
+    for (int k = 0; k < REG; k++) {
+        const uint32_t j = l + 16 * k;
+        v[k] = j < T ? x[j] : 0.0f;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < REG; k++)
+        if (l + 16 * k < T)
+            m = __builtin_fmaxf(m, v[k] * scale);
+    m = __builtin_fmaxf(m, __shfl_xor(m, 8, 16));
+    m = __builtin_fmaxf(m, __shfl_xor(m, 4, 16));
+    m = __builtin_fmaxf(m, __shfl_xor(m, 2, 16));
+    m = __builtin_fmaxf(m, __shfl_xor(m, 1, 16));
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < REG; k++) {
+        const uint32_t j = l + 16 * k;
+        if (j < T) {
+            const float e = pk_expf(v[k] * scale - m);
+            x[j] = e;
+            acc += e;
+        }
+    }
+    const float r = 1.0f / lanes16_sum(acc);
+    if (l == 0)
+        inv[row] = r;
+}
+
 constexpr int kPI = 32, kPD = 32, kPJ = 32;    /* queries, dimensions, keys a stage of PV */
 
 __global__ __launch_bounds__(128) void att_pv_kernel(float *__restrict__ of, const float *__restrict__ S,
@@ -803,7 +843,12 @@ int launch_attention(float *of, float *ws, const float *qf, const float *kf, con
         att_dims_kernel<true><<<dim3((T + kSQ - 1 + kSY - 1) / kSY, qt, H), 256, 0, s>>>(S, Ts, qf, pf, bv, T, D, dk);
     }
     const float scale = 1.0f / sqrtf((float)dk);
-    att_softmax_kernel<<<(rows + 15) / 16, 256, 0, s>>>(S, inv, Ts, rows, T, scale);
+    if (T <= 16 * 16)
+        att_softmax_reg_kernel<16><<<(rows + 15) / 16, 256, 0, s>>>(S, inv, Ts, rows, T, scale);
+    else if (T <= 16 * 64)
+        att_softmax_reg_kernel<64><<<(rows + 15) / 16, 256, 0, s>>>(S, inv, Ts, rows, T, scale);
+    else
+        att_softmax_kernel<<<(rows + 15) / 16, 256, 0, s>>>(S, inv, Ts, rows, T, scale);
     if (g_att_valu)
         att_pv_kernel<<<dim3(dk / kPD, (T + kPI - 1) / kPI, H), 128, 0, s>>>(of, S, inv, Ts, vf, T, D, dk);
     else
