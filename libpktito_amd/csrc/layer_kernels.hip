@@ -731,15 +731,25 @@ __global__ __launch_bounds__(256) void dwq_kernel(int8_t *__restrict__ qp, float
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int64_t half = K / 2;
     const uint32_t rows = 16 + K - 1;
-    for (uint32_t e = tid; e < rows * 64; e += 256) {
-        const uint32_t r = e / 64, c = e % 64;
+    /* GLU of the frames the taps reach: every load of a thread issued before
+     * the first gate (one memory round trip), then h = a * sigmoid(g) */
+    constexpr int kPT = (16 + kMaxTaps - 1) * 64 / 256;
+    float ua[kPT], ug[kPT];
+#pragma unroll
+    for (int k = 0; k < kPT; k++) {
+        const uint32_t e = tid + 256 * k, r = e / 64, c = e % 64;
         const int64_t s = (int64_t)t0 - half + r;
-        float hv = 0.0f;
-        if (s >= 0 && s < (int64_t)T) {
-            const float *us = u + (size_t)s * 2 * D + c0 + c;
-            hv = us[0] * pk_sigmoidf(us[D]);
-        }
-        hs[r][c] = hv;
+        const bool in = e < rows * 64 && s >= 0 && s < (int64_t)T;
+        const float *us = u + (size_t)(in ? s : 0) * 2 * D + c0 + c;
+        ua[k] = in ? us[0] : 0.0f;
+        ug[k] = in ? us[D] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < kPT; k++) {
+        const uint32_t e = tid + 256 * k, r = e / 64, c = e % 64;
+        const int64_t s = (int64_t)t0 - half + r;
+        if (e < rows * 64)
+            hs[r][c] = s >= 0 && s < (int64_t)T ? ua[k] * pk_sigmoidf(ug[k]) : 0.0f;
     }
     __syncthreads();
     const uint32_t c = c0 + lane;
