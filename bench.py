@@ -66,6 +66,8 @@ def parse():
                    help="only launch the named product's kernel 50 times (for rocprofv3 --pmc runs)")
     p.add_argument("--profile-layer", type=int, default=0, metavar="QB",
                    help="only replay the device-resident layer at M=750 in blocks of QB (for rocprofv3)")
+    p.add_argument("--profile-decoder", action="store_true",
+                   help="the decoder's token steps only (graphs of a prediction and a joint, no CPU leg)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy 256 MiB three times (the known-size kernel that scales "
                         "rocprofv3's FETCH_SIZE / WRITE_SIZE)")
@@ -545,7 +547,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run "
-              "(the int8 path would shard frames across GPUs with no exchange, DESIGN.md)", file=sys.stderr)
+              "(the int8 path would shard frames across GPUs with no exchange)", file=sys.stderr)
         sys.exit(2)
     import torch
     if args.copy_calibration:
@@ -561,6 +563,9 @@ def main():
     torch.cuda.set_device(0)
 
     M = 750
+    if args.profile_decoder:
+        print(json.dumps({"profiled": "decoder_steps", **decoder_steps(pk, torch, False)}))
+        return
     if args.profile_layer:
         us, _ = device_layer(pk, torch, M, args.profile_layer, reps=args.steps, warmup=args.warmup)
         print(json.dumps({"profiled": "device_layer", "M": M, "qb": args.profile_layer, "us_per_layer": round(us, 1),
