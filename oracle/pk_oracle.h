@@ -3,8 +3,9 @@
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product (libpktito_amd/) links,
  * loads or calls this code; only tests/, the smoke check of
- * __graft_entry__.py and bench.py's cpu_baseline leg do, and only as the
- * checker or as the baseline being timed, never as the thing measured.
+ * __graft_entry__.py and bench.py's cpu_baseline leg do, and only as what
+ * the results are compared with or as the baseline being timed, never as the
+ * thing measured.
  *
  * What each function restates (file:line in peterheb/libpktito 0.9.8):
  *

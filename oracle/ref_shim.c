@@ -1,5 +1,5 @@
-/* A handle on the reference's own compiled backends, for the checker and the
- * CPU baseline. Test infrastructure only (see pk_oracle.h).
+/* A handle on the reference's own compiled backends, for the parity tests
+ * and the CPU baseline. Test infrastructure only (see pk_oracle.h).
  *
  * oracle/Makefile compiles this file together with the reference's
  * backend/ref/kernels.c and its x86 backends, in place under the reference

@@ -1,6 +1,7 @@
 """ctypes handles on the oracle (oracle/liboracle.so, the CPU restatement) and,
 where it was built, the reference's own compiled backends (oracle/_ref/
-libpkref.so). Test infrastructure: the checker, never the thing measured."""
+libpkref.so). Test infrastructure: what the tests compare against, never the
+thing measured."""
 import ctypes
 import os
 import subprocess

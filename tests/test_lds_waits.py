@@ -13,7 +13,7 @@ import lds_waits
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def test_checker_catches_a_copy_before_the_wait():
+def test_analysis_catches_a_copy_before_the_wait():
     body = """
         ds_read_b128 v[4:7], v1
         ds_read_b128 v[8:11], v2
@@ -28,7 +28,7 @@ def test_checker_catches_a_copy_before_the_wait():
     assert [t for t, _ in bad] == ["v_mov_b32_e32 v21, v9"]
 
 
-def test_checker_follows_loops_and_joins():
+def test_analysis_follows_loops_and_joins():
     # the read issued at the bottom of the loop is in flight at its top
     body = """
         s_waitcnt lgkmcnt(0)
