@@ -828,6 +828,15 @@ __device__ __forceinline__ v4i lds_read16(uint32_t addr) {
     return r;
 }
 
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+/* 8 bytes from LDS, as lds_read16 */
+__device__ __forceinline__ v2i lds_read8(uint32_t addr) {
+    v2i r;
+    asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+    return r;
+}
+
 /* f(integral_constant<int, I>) for I in [I0, N), unrolled at compile time */
 template <int I, int N, typename F>
 __device__ __forceinline__ void for_static(F &&f) {
@@ -1062,9 +1071,9 @@ __device__ __forceinline__ float lds_read4(uint32_t addr) {
 
 /* BLK: 0, a block a column (qb == n); 1, blocks of one unit (qb == 64);
  * 2, blocks of half a unit (qb == 32). With blocks, each block's exact int32
- * sum comes from MFMAs of its own (a unit's two halves by masking the weight
- * fragment to the lanes holding that half's inputs, lanes 0-31 holding
- * inputs 0-31 of the unit and lanes 32-63 the rest), and enters ref's chain
+ * sum comes from MFMAs of its own (with blocks of 32, a 16x16x32 MFMA on each
+ * half of the unit, its 8 bytes a lane read from LDS where the unit holds
+ * them), and enters ref's chain
  * acc = fmaf((float)s, d, acc) in block order; blocks past n (padding units)
  * are skipped. The stage's block scales ride with its units: each slot ends
  * with BM frames x the stage's blocks of d, frame-contiguous, loaded by DMA
@@ -1178,8 +1187,14 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
         for (int j = 0; j < (BLK ? TM : 1); j++)
             accf[i][j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
-    const uint32_t wbase = lds_addr(ring) + (wn * TN) * kUnitBytes + lane * 16;
-    const uint32_t abase = lds_addr(ring) + (UB + wm * TM) * kUnitBytes + lane * 16;
+    /* With blocks of 32 (BLK 2) a lane reads, for each half h of a unit (one
+     * block), the 8 bytes the 16x16x32 MFMA takes from it: row lane % 16,
+     * inputs 32 h + 8 (lane / 16) .. + 7, which the unit holds at
+     * ((2 h + lane / 32) 16 + lane % 16) 16 + 8 ((lane / 16) % 2); the bytes
+     * of half h are 512 h further on. Otherwise a lane's 16-byte slot. */
+    const uint32_t lofs = BLK == 2 ? ((lane >> 5) * 16 + (lane & 15)) * 16 + ((lane >> 4) & 1) * 8 : lane * 16;
+    const uint32_t wbase = lds_addr(ring) + (wn * TN) * kUnitBytes + lofs;
+    const uint32_t abase = lds_addr(ring) + (UB + wm * TM) * kUnitBytes + lofs;
     /* this lane's frame within the tile for frame tile j: (wm TM + j) 16 + lane % 16 */
     const uint32_t dbase = lds_addr(ring) + SLOTU * kUnitBytes + ((wm * TM) * 16 + (lane & 15)) * 4;
     /* LDS offset of sub-step gi's fragments */
@@ -1193,12 +1208,26 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
     };
     auto read_set = [&](Set &st, uint32_t gi) {
         const uint32_t at = at_of(gi);
+        if constexpr (BLK == 2) {
+            /* f = { block 0's 8 bytes, block 1's 8 bytes } */
 #pragma unroll
-        for (int i = 0; i < TN; i++)
-            st.f[i] = lds_read16(wbase + at + i * kUnitBytes);
+            for (int i = 0; i < TN; i++) {
+                const v2i lo = lds_read8(wbase + at + i * kUnitBytes), hi = lds_read8(wbase + at + i * kUnitBytes + 512);
+                st.f[i] = v4i{ lo.x, lo.y, hi.x, hi.y };
+            }
 #pragma unroll
-        for (int j = 0; j < TM; j++)
-            st.f[TN + j] = lds_read16(abase + at + j * kUnitBytes);
+            for (int j = 0; j < TM; j++) {
+                const v2i lo = lds_read8(abase + at + j * kUnitBytes), hi = lds_read8(abase + at + j * kUnitBytes + 512);
+                st.f[TN + j] = v4i{ lo.x, lo.y, hi.x, hi.y };
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+                st.f[i] = lds_read16(wbase + at + i * kUnitBytes);
+#pragma unroll
+            for (int j = 0; j < TM; j++)
+                st.f[TN + j] = lds_read16(abase + at + j * kUnitBytes);
+        }
         if constexpr (BLK != 0) {
             const uint32_t s = gi / UPS, kk = gi % UPS;
 #pragma unroll
@@ -1243,23 +1272,20 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
             const uint32_t u = u0 + gi;             /* the unit: uniform */
 #pragma unroll
             for (int h = 0; h < BPU; h++) {
-                v4i fw[TN];
-#pragma unroll
-                for (int i = 0; i < TN; i++) {
-                    if constexpr (BLK == 2) {
-                        const bool mine = (lane >> 5) == h;
-                        fw[i] = v4i{mine ? cur.f[i][0] : 0, mine ? cur.f[i][1] : 0, mine ? cur.f[i][2] : 0,
-                                    mine ? cur.f[i][3] : 0};
-                    } else {
-                        fw[i] = cur.f[i];
-                    }
-                }
 #pragma unroll
                 for (int i = 0; i < TN; i++)
 #pragma unroll
-                    for (int j = 0; j < TM; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fw[i], cur.f[TN + j], v4i{0, 0, 0, 0}, 0,
-                                                                          0, 0);
+                    for (int j = 0; j < TM; j++) {
+                        if constexpr (BLK == 2) {
+                            /* block h alone: its 32 inputs, 8 bytes a lane */
+                            const long wh = __builtin_bit_cast(long, v2i{ cur.f[i][2 * h], cur.f[i][2 * h + 1] });
+                            const long ah = __builtin_bit_cast(long, v2i{ cur.f[TN + j][2 * h], cur.f[TN + j][2 * h + 1] });
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wh, ah, v4i{0, 0, 0, 0}, 0, 0, 0);
+                        } else {
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.f[i], cur.f[TN + j],
+                                                                              v4i{0, 0, 0, 0}, 0, 0, 0);
+                        }
+                    }
                 if (u * BPU + h < nb) {
 #pragma unroll
                     for (int i = 0; i < TN; i++)
