@@ -107,6 +107,16 @@ pk_hip_q8 *holding(const void *p) {
     return a < it->first + (uintptr_t)m->rows * m->cols ? m : nullptr;
 }
 
+/* whether [p, p + len) shares a byte with an uploaded matrix's host bytes;
+ * caller holds g_reg_mu */
+bool overlaps(const void *p, size_t len) {
+    const uintptr_t a = (uintptr_t)p;
+    if (holding(p))
+        return true;
+    auto it = g_reg.lower_bound(a);         /* a matrix starting inside the range */
+    return it != g_reg.end() && it->first < a + len;
+}
+
 void free_matrix(pk_hip_q8 *m) {
     (void)hipSetDevice(g_dev);
     (void)hipFree(m->w);
@@ -443,7 +453,7 @@ int pk_hip_upload_q8(const int8_t *q, const float *s, uint32_t rows, uint32_t co
                                    "16384 inputs; not %u x %u", rows, cols);
     {
         std::shared_lock<std::shared_mutex> lk(g_reg_mu);
-        if (holding(q) || holding(q + (size_t)rows * cols - 1))
+        if (overlaps(q, (size_t)rows * cols))
             return fail(PK_HIP_EINVAL, "upload: host bytes at %p overlap an uploaded matrix", (const void *)q);
     }
     PK_TRY(hipSetDevice(g_dev));
@@ -471,6 +481,11 @@ int pk_hip_upload_q8(const int8_t *q, const float *s, uint32_t rows, uint32_t co
         return hip_fail(he, "upload");
     }
     std::unique_lock<std::shared_mutex> lk(g_reg_mu);
+    if (overlaps(q, (size_t)rows * cols)) {     /* another thread uploaded these bytes meanwhile */
+        lk.unlock();
+        free_matrix(m);
+        return fail(PK_HIP_EINVAL, "upload: host bytes at %p overlap an uploaded matrix", (const void *)q);
+    }
     g_reg[(uintptr_t)q] = m;
     return PK_HIP_OK;
 }

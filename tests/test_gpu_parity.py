@@ -167,6 +167,23 @@ def test_rounding_modes(hip, rmode):
     assert e.value.code == hip.PK_HIP_EROUND
 
 
+def test_upload_rejects_overlapping_bytes(hip):
+    """The registry is keyed on host bytes, so an upload whose bytes share any
+    byte with an uploaded matrix is refused: one that contains it whole, one
+    that starts inside it, one that ends inside it; a disjoint one is taken."""
+    buf = np.zeros(64 * 64, np.int8)
+    s16, s64 = np.ones(16, np.float32), np.ones(64, np.float32)
+    with hip.Q8Matrix(buf[16 * 64:32 * 64], s16):
+        for view, sc in ((buf, s64), (buf[20 * 64:36 * 64], s16), (buf[4 * 64:20 * 64], s16)):
+            with pytest.raises(hip.PkHipError) as e:
+                hip.Q8Matrix(view, sc)
+            assert e.value.code == hip.PK_HIP_EINVAL
+        with hip.Q8Matrix(buf[32 * 64:48 * 64], s16):
+            pass
+    with hip.Q8Matrix(buf, s64):
+        pass
+
+
 # --------------------------------------------- the measured shapes, whole ---
 
 def test_single_product_full_size(hip):
