@@ -49,6 +49,14 @@ int hip_fail(hipError_t e, const char *what) {
     return fail(PK_HIP_EDEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
+/* A launcher's nonzero return: -2 sizes no kernel takes (nothing launched),
+ * otherwise the HIP error the launch left. */
+int launch_fail(int r, const char *what) {
+    if (r == -2)
+        return fail(PK_HIP_EINVAL, "%s: the sizes fit no kernel", what);
+    return hip_fail(hipGetLastError(), what);
+}
+
 #define PK_TRY(call)                                          \
     do {                                                      \
         hipError_t e_ = (call);                               \
@@ -325,8 +333,8 @@ int check_act(const pk_hip_act *a, bool for_gemm) {
 
 int launch_quant(pk_hip_act *a, const float *x, size_t xs, hipStream_t s) {
     const char *name = "";
-    if (pkq8::launch_quantize(a->q, a->d, x, xs, a->n, a->qb, a->T, s, &name))
-        return hip_fail(hipGetLastError(), "quantize launch");
+    if (const int r = pkq8::launch_quantize(a->q, a->d, x, xs, a->n, a->qb, a->T, s, &name))
+        return launch_fail(r, "quantize launch");
     g_kernel = name;
     return PK_HIP_OK;
 }
@@ -362,7 +370,7 @@ int launch_product_siluq(const pk_hip_q8 *m, const pk_hip_act *a, const int8_t *
     if (r == -3)
         return 1;
     if (r)
-        return -hip_fail(hipGetLastError(), "gemm_q8 silu-quantized launch");
+        return -launch_fail(r, "gemm_q8 silu-quantized launch");
     g_kernel = name;
     return 0;
 }
@@ -388,8 +396,8 @@ int launch_product(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint3
     tab.s[0] = pkq8::Seg{ out, qp ? qp : a->q, a->d, (uint64_t)os,
                           qp ? (uint64_t)pkq8::packed_groups(a->T) * pkq8::kUnitBytes : 0, a->T, 0 };
     const char *name = "";
-    if (pkq8::launch_gemm(g, tab, s, &name))
-        return hip_fail(hipGetLastError(), "gemm_q8 launch");
+    if (const int r = pkq8::launch_gemm(g, tab, s, &name))
+        return launch_fail(r, "gemm_q8 launch");
     g_kernel = name;
     return PK_HIP_OK;
 }
@@ -672,8 +680,8 @@ int pk_hip_quantize_packed_dev(pk_hip_act *a, int8_t *qp, const float *x, size_t
     if (xs < a->n || xs % 4 || ((uintptr_t)x & 15) || ((uintptr_t)qp & 15) || ((uintptr_t)a->q & 15))
         return fail(PK_HIP_EINVAL, "quantize_packed_dev: x, q and qp 16-byte aligned, xs >= n and a multiple of 4");
     const char *name = "";
-    if (pkq8::launch_quantize_packed(a->q, qp, a->d, x, xs, a->n, a->qb, a->T, (hipStream_t)stream, &name))
-        return hip_fail(hipGetLastError(), "quantize_packed launch");
+    if (const int r = pkq8::launch_quantize_packed(a->q, qp, a->d, x, xs, a->n, a->qb, a->T, (hipStream_t)stream, &name))
+        return launch_fail(r, "quantize_packed launch");
     g_kernel = name;
     return PK_HIP_OK;
 }
@@ -751,8 +759,8 @@ int pk_hip_gemm_q8_batch_dev(const pk_hip_job *jobs, uint32_t njobs, int rmode, 
                               (uint64_t)pkq8::packed_groups(a->T) * pkq8::kUnitBytes, a->T, 0 };
     }
     const char *name = "";
-    if (pkq8::launch_gemm_batch(tab, (hipStream_t)stream, &name))
-        return hip_fail(hipGetLastError(), "gemm_q8_batch_dev launch");
+    if (const int r = pkq8::launch_gemm_batch(tab, (hipStream_t)stream, &name))
+        return launch_fail(r, "gemm_q8_batch_dev launch");
     g_kernel = name;
     return PK_HIP_OK;
 }
@@ -803,8 +811,8 @@ int pk_hip_gemm_q8_grouped_dev(const pk_hip_q8 *m, uint32_t r0, uint32_t rows, c
     g.add = add;
     g.rmode = 0;
     const char *name = "";
-    if (pkq8::launch_gemm(g, tab, (hipStream_t)stream, &name))
-        return hip_fail(hipGetLastError(), "gemm_q8_grouped launch");
+    if (const int r = pkq8::launch_gemm(g, tab, (hipStream_t)stream, &name))
+        return launch_fail(r, "gemm_q8_grouped launch");
     g_kernel = name;
     return PK_HIP_OK;
 }
@@ -823,8 +831,8 @@ bool blocks_ok(const pk_hip_act *a, bool whole) {
 
 #define PK_LAUNCH(call, what)                                            \
     do {                                                                 \
-        if ((call))                                                      \
-            return hip_fail(hipGetLastError(), what);                    \
+        if (const int r_ = (call))                                       \
+            return launch_fail(r_, what);                                \
     } while (0)
 
 /* The layer's workspace, carved in 256-byte aligned pieces; with base NULL

@@ -1921,8 +1921,8 @@ int launch_gemm_batch(const JobTable &jobs, hipStream_t s, const char **name) {
         SegTable t;
         t.nseg = 1;
         t.s[0] = jobs.s[j];
-        if (launch_gemm(jobs.g[j], t, s, name))
-            return -1;
+        if (const int r = launch_gemm(jobs.g[j], t, s, name))
+            return r;
     }
     return 0;
 }
