@@ -726,6 +726,7 @@ __global__ __launch_bounds__(256) void dwq_kernel(int8_t *__restrict__ qp, float
                                                   const float *__restrict__ w, const float *__restrict__ b,
                                                   uint32_t K) {
     __shared__ float hs[16 + kMaxTaps - 1][64];
+    __shared__ float wl[kMaxTaps][64];
     __shared__ __attribute__((aligned(16))) int8_t unit[kUnitBytes];
     const uint32_t g = blockIdx.x, G = gridDim.x, c0 = blockIdx.y * 64, t0 = 16 * g;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -744,6 +745,9 @@ __global__ __launch_bounds__(256) void dwq_kernel(int8_t *__restrict__ qp, float
         ua[k] = in ? us[0] : 0.0f;
         ug[k] = in ? us[D] : 0.0f;
     }
+    /* the 64 channels' taps, tap-major */
+    for (uint32_t e = tid; e < K * 64; e += 256)
+        wl[e / 64][e % 64] = w[(size_t)(c0 + e % 64) * K + e / 64];
 #pragma unroll
     for (int k = 0; k < kPT; k++) {
         const uint32_t e = tid + 256 * k, r = e / 64, c = e % 64;
@@ -754,21 +758,38 @@ __global__ __launch_bounds__(256) void dwq_kernel(int8_t *__restrict__ qp, float
     __syncthreads();
     const uint32_t c = c0 + lane;
     const float bc = b[c];
-    const float *wc = w + (size_t)c * K;
+    /* the wave's four frames side by side, each its own chain over the taps
+     * in order (the taps past the ends skipped), so the four chains' steps
+     * overlap */
+    float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+    for (uint32_t j = 0; j < K; j++) {
+        const float wj = wl[j][lane];
+#pragma unroll
+        for (int f = 0; f < 4; f++) {
+            const uint32_t r = 4 * wv + f;
+            const int64_t s = (int64_t)t0 + r + j - half;
+            if (s >= 0 && s < (int64_t)T)
+                acc[f] = __builtin_fmaf(wj, hs[r + j][lane], acc[f]);
+        }
+    }
+    /* the four frames' SiLU and block maxima, independent of each other */
+    float y[4];
+    uint32_t mbs[4];
+#pragma unroll
+    for (int f = 0; f < 4; f++) {
+        y[f] = 0.0f;
+        if (t0 + 4 * wv + f < T) {
+            const float v = acc[f] + bc;
+            y[f] = v * pk_sigmoidf(v);
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < 4; f++)
+        mbs[f] = (uint32_t)(QB == 64 ? wave_max_nonneg(mag_bits(y[f])) : half_max_nonneg(mag_bits(y[f]), lane));
+#pragma unroll
     for (int f = 0; f < 4; f++) {
         const uint32_t r = 4 * wv + f, t = t0 + r;
-        float y = 0.0f;
-        if (t < T) {
-            float acc = 0.0f;
-            for (uint32_t j = 0; j < K; j++) {
-                const int64_t s = (int64_t)t + j - half;
-                if (s >= 0 && s < (int64_t)T)
-                    acc = __builtin_fmaf(wc[j], hs[r + j][lane], acc);
-            }
-            const float v = acc + bc;
-            y = v * pk_sigmoidf(v);
-        }
-        const uint32_t mb = (uint32_t)(QB == 64 ? wave_max_nonneg(mag_bits(y)) : half_max_nonneg(mag_bits(y), lane));
+        const uint32_t mb = mbs[f];
         const bool zero = zero_bits(mb);
         float dv = 0.0f, id = 0.0f;
         if (!zero) {
@@ -776,7 +797,7 @@ __global__ __launch_bounds__(256) void dwq_kernel(int8_t *__restrict__ qp, float
             dv = amax / 127.0f;
             id = 127.0f / amax;
         }
-        unit[in_unit(lane, r)] = (int8_t)(zero ? 0 : q1(y, id));
+        unit[in_unit(lane, r)] = (int8_t)(zero ? 0 : q1(y[f], id));
         if (t < T && lane % QB == 0)
             d[(size_t)t * (D / QB) + c / QB] = dv;
     }
