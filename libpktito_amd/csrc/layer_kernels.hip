@@ -65,18 +65,35 @@ __device__ __forceinline__ float4 normed(float4 v, float mean, float r, float4 w
 
 /* A wave's frame of n <= 256 CH floats: loaded once as float4 chunks
  * i + 64 c into registers and into the wave's LDS row, then its mean and
- * 1 / sqrt(var + eps) from the row. */
+ * 1 / sqrt(var + eps) from the row. The same chunks of the norm's weights
+ * and biases are loaded into wc and bc behind the frame's, so they arrive
+ * while the sums run. */
 template <int CH>
 __device__ __forceinline__ void frame_stats(const float *__restrict__ xr, float *row, uint32_t n, float eps,
-                                            int lane, float4 (&v)[CH], float &mean, float &r) {
+                                            int lane, float4 (&v)[CH], float &mean, float &r,
+                                            const float *__restrict__ w, const float *__restrict__ b,
+                                            float4 (&wc)[CH], float4 (&bc)[CH]) {
     const uint32_t n4 = n >> 2;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
-        if (i < n4) {
+        if (i < n4)
             v[c] = ((const float4 *)xr)[i];
-            ((float4 *)row)[i] = v[c];
+    }
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        wc[c] = bc[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < n4) {
+            wc[c] = ((const float4 *)w)[i];
+            bc[c] = ((const float4 *)b)[i];
         }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t i = lane + 64 * c;
+        if (i < n4)
+            ((float4 *)row)[i] = v[c];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -103,15 +120,14 @@ __global__ __launch_bounds__(256) void normq_kernel(int8_t *__restrict__ qp, flo
     const uint32_t t = blockIdx.x * 4 + wv;
     if (t >= T)
         return;
-    float4 v[CH];
+    float4 v[CH], wc[CH], bc[CH];
     float mean, r;
-    frame_stats<CH>(x + (size_t)t * n, rows[wv], n, eps, lane, v, mean, r);
+    frame_stats<CH>(x + (size_t)t * n, rows[wv], n, eps, lane, v, mean, r, w, b, wc, bc);
     const uint32_t n4 = n >> 2;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
-        v[c] = i < n4 ? normed(v[c], mean, r, ((const float4 *)w)[i], ((const float4 *)b)[i])
-                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[c] = i < n4 ? normed(v[c], mean, r, wc[c], bc[c]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     const WaveScales<CH, QB> sc(v);
     const uint32_t G = (T + 15) / 16, g = t >> 4, fr = t & 15;
@@ -142,15 +158,15 @@ __global__ __launch_bounds__(256) void norm_kernel(float *__restrict__ x, uint32
     if (t >= T)
         return;
     float *xr = x + (size_t)t * n;
-    float4 v[CH];
+    float4 v[CH], wc[CH], bc[CH];
     float mean, r;
-    frame_stats<CH>(xr, rows[wv], n, eps, lane, v, mean, r);
+    frame_stats<CH>(xr, rows[wv], n, eps, lane, v, mean, r, w, b, wc, bc);
     const uint32_t n4 = n >> 2;
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
         if (i < n4)
-            ((float4 *)xr)[i] = normed(v[c], mean, r, ((const float4 *)w)[i], ((const float4 *)b)[i]);
+            ((float4 *)xr)[i] = normed(v[c], mean, r, wc[c], bc[c]);
     }
 }
 
