@@ -32,20 +32,27 @@ __device__ __forceinline__ float4 row4(const float *__restrict__ x, uint32_t i, 
     return make_float4(x[k], k + 1 < n ? x[k + 1] : 0.0f, k + 2 < n ? x[k + 2] : 0.0f, k + 3 < n ? x[k + 3] : 0.0f);
 }
 
-/* One row of n <= 256 CH values quantized whole by one wave into q (LDS,
- * bytes, zero to 64 kr, kr <= 4 CH): every lane loads its chunks i + 64 c
- * first (value4(i) gives chunk i, zeros past n), so the row costs one
- * memory round trip. Returns d (the block rule on magnitude bits: a NaN or
- * an infinity, or an amax below 2^-121, makes the row zero). */
+/* One row of n <= 256 CH values, quantized whole by one wave into q (LDS,
+ * bytes, zero to 64 kr, kr <= 4 CH) in two steps. load_row: every lane
+ * issues the loads of its chunks i + 64 c (value4(i) gives chunk i, zeros
+ * past n), so the row costs one memory round trip, and the caller may
+ * issue other loads behind them before it uses the row. */
 template <int CH, typename F>
-__device__ __forceinline__ float quant_row(F value4, uint32_t n, uint32_t kr, int8_t *q, int lane) {
+__device__ __forceinline__ void load_row(F value4, uint32_t n, int lane, float4 (&v)[CH]) {
     const uint32_t n4 = (n + 3) >> 2;
-    float4 v[CH];
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
         v[c] = i < n4 ? value4(i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+}
+
+/* quant_loaded: the loaded row quantized into q. Returns d (the block rule
+ * on magnitude bits: a NaN or an infinity, or an amax below 2^-121, makes
+ * the row zero). */
+template <int CH>
+__device__ __forceinline__ float quant_loaded(const float4 (&v)[CH], uint32_t n, uint32_t kr, int8_t *q, int lane) {
+    const uint32_t n4 = (n + 3) >> 2;
     const WaveScales<CH, 0> sc(v);
 #pragma unroll
     for (int c = 0; c < CH; c++) {
@@ -57,20 +64,24 @@ __device__ __forceinline__ float quant_row(F value4, uint32_t n, uint32_t kr, in
 }
 
 /* The exact int32 sums of the 16 rows of panel p over units [0, kr), kr <=
- * KU: lane l takes row l % 16 and inputs 16 (l / 16) .. + 15 of each unit
- * (the unit's bytes 16 l .. 16 l + 15: the wave reads each 1 KB unit whole,
- * every unit's load issued before the first sum), the four lanes of a row
- * add up by shuffles. Every lane returns its row's sum. */
+ * KU, in two steps. panel_load: lane l loads the unit's bytes 16 l .. 16 l
+ * + 15 of each unit (the wave reads each 1 KB unit whole, every unit's load
+ * issued before the first sum). panel_sum: lane l takes row l % 16 and
+ * inputs 16 (l / 16) .. + 15 of each unit, and the four lanes of a row add
+ * up by shuffles; every lane returns its row's sum. */
 template <int KU>
-__device__ __forceinline__ int panel_dot(const int8_t *__restrict__ w, uint64_t wstride, uint32_t p, uint32_t kr,
-                                         const int8_t *q, int lane) {
+__device__ __forceinline__ void panel_load(const int8_t *__restrict__ w, uint64_t wstride, uint32_t p, uint32_t kr,
+                                           int lane, v4i (&wv)[KU]) {
     const int8_t *wp = w + (size_t)p * kUnitBytes + lane * 16;
-    const int8_t *qp = q + (lane >> 4) * 16;
-    v4i wv[KU];
 #pragma unroll
     for (int u = 0; u < KU; u++)
         if (u < (int)kr)
             wv[u] = *(const v4i *)(wp + (size_t)u * wstride);
+}
+
+template <int KU>
+__device__ __forceinline__ int panel_sum(const v4i (&wv)[KU], uint32_t kr, const int8_t *q, int lane) {
+    const int8_t *qp = q + (lane >> 4) * 16;
     int s = 0;
 #pragma unroll
     for (int u = 0; u < KU; u++)
@@ -86,13 +97,28 @@ __device__ __forceinline__ int panel_dot(const int8_t *__restrict__ w, uint64_t 
     return s;
 }
 
+/* Whether a kernel of KU units a panel loads its panels behind its row,
+ * before the quantize (one memory round trip instead of two): where the
+ * panels fit the registers beside the row (the 64-unit kernels load them
+ * after). */
+template <int KU>
+constexpr bool kEarly = KU <= 16;
+
+template <int KU>
+__device__ __forceinline__ int panel_dot(const int8_t *__restrict__ w, uint64_t wstride, uint32_t p, uint32_t kr,
+                                         const int8_t *q, int lane) {
+    v4i wv[KU];
+    panel_load<KU>(w, wstride, p, kr, lane, wv);
+    return panel_sum<KU>(wv, kr, q, lane);
+}
+
 /* gemm_q8's epilogue for one output of a one-block row
  * (backend/ref/kernels.c:75-84): fmaf((float)s, d, +0), times ws, plus the
- * bias */
-__device__ __forceinline__ float gemv_out(int s, float d, float ws, const float *bias, uint32_t r) {
+ * bias br where there is a bias */
+__device__ __forceinline__ float gemv_out(int s, float d, float ws, const float *bias, float br) {
     float v = __builtin_fmaf((float)s, d, 0.0f) * ws;
     if (bias)
-        v = v + bias[r];
+        v = v + br;
     return v;
 }
 
@@ -107,13 +133,21 @@ __global__ __launch_bounds__(64) void gemv_kernel(float *__restrict__ out, const
     __shared__ __attribute__((aligned(16))) int8_t q[64 * KU];
     const int lane = threadIdx.x;
     const uint32_t p = blockIdx.x;
-    const float d = quant_row<CH>([&](uint32_t i) { return row4<AL>(x, i, n); }, n, kr, q, lane);
+    float4 v[CH];
+    load_row<CH>([&](uint32_t i) { return row4<AL>(x, i, n); }, n, lane, v);
+    v4i wv[KU];
+    if constexpr (kEarly<KU>)
+        panel_load<KU>(w, wstride, p, kr, lane, wv);
+    const uint32_t r = 16 * p + (lane & 15);
+    const float wsr = ws[r], br = bias ? bias[r] : 0.0f, old = add ? out[r] : 0.0f;
+    const float d = quant_loaded<CH>(v, n, kr, q, lane);
     __syncthreads();
-    const int s = panel_dot<KU>(w, wstride, p, kr, q, lane);
+    if constexpr (!kEarly<KU>)
+        panel_load<KU>(w, wstride, p, kr, lane, wv);
+    const int s = panel_sum<KU>(wv, kr, q, lane);
     if (lane < 16) {
-        const uint32_t r = 16 * p + lane;
-        const float v = gemv_out(s, d, ws[r], bias, r);
-        out[r] = add ? out[r] + v : v;
+        const float o = gemv_out(s, d, wsr, bias, br);
+        out[r] = add ? old + o : o;
     }
 }
 
@@ -134,23 +168,44 @@ __global__ __launch_bounds__(256) void lstm_kernel(float *__restrict__ h_out, fl
     __shared__ float dq[2], gates[4][16];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t j0 = 16 * blockIdx.x;
+    /* every load the step needs is issued before the first use: the row
+     * (waves 0 and 1), the gate's two panels, the scales, the bias, c */
+    float4 v[CH];
+    if (wv == 0)
+        load_row<CH>([&](uint32_t i) { return row4<AL>(x, i, P); }, P, lane, v);
+    else if (wv == 1)
+        load_row<CH>([&](uint32_t i) { return row4<AL>(h_in, i, P); }, P, lane, v);
+    const uint32_t p = (wv * P + j0) / 16;
+    constexpr int KE = kEarly<KU> ? KU : 1;       /* late: one panel's registers at a time */
+    v4i wxv[KE], whv[KE];
+    if constexpr (kEarly<KU>) {
+        panel_load<KU>(wx, wstride, p, kr, lane, wxv);
+        panel_load<KU>(wh, wstride, p, kr, lane, whv);
+    }
+    const uint32_t r = wv * P + j0 + (lane & 15);
+    const float wxsr = wxs[r], whsr = whs[r], br = b ? b[r] : 0.0f;
+    const float cold = threadIdx.x < 16 ? c[j0 + threadIdx.x] : 0.0f;
     if (wv == 0) {
-        const float d = quant_row<CH>([&](uint32_t i) { return row4<AL>(x, i, P); }, P, kr, qx, lane);
+        const float d = quant_loaded<CH>(v, P, kr, qx, lane);
         if (lane == 0)
             dq[0] = d;
     } else if (wv == 1) {
-        const float d = quant_row<CH>([&](uint32_t i) { return row4<AL>(h_in, i, P); }, P, kr, qh, lane);
+        const float d = quant_loaded<CH>(v, P, kr, qh, lane);
         if (lane == 0)
             dq[1] = d;
     }
     __syncthreads();
-    const uint32_t p = (wv * P + j0) / 16;
-    const int sx = panel_dot<KU>(wx, wstride, p, kr, qx, lane);
-    const int sh = panel_dot<KU>(wh, wstride, p, kr, qh, lane);
+    int sx, sh;
+    if constexpr (kEarly<KU>) {
+        sx = panel_sum<KU>(wxv, kr, qx, lane);
+        sh = panel_sum<KU>(whv, kr, qh, lane);
+    } else {
+        sx = panel_dot<KU>(wx, wstride, p, kr, qx, lane);
+        sh = panel_dot<KU>(wh, wstride, p, kr, qh, lane);
+    }
     if (lane < 16) {
-        const uint32_t r = wv * P + j0 + lane;
-        const float g = gemv_out(sx, dq[0], wxs[r], b, r);
-        gates[wv][lane] = g + gemv_out(sh, dq[1], whs[r], nullptr, r);
+        const float g = gemv_out(sx, dq[0], wxsr, b, br);
+        gates[wv][lane] = g + gemv_out(sh, dq[1], whsr, nullptr, 0.0f);
     }
     __syncthreads();
     if (threadIdx.x < 16) {
@@ -159,7 +214,7 @@ __global__ __launch_bounds__(256) void lstm_kernel(float *__restrict__ h_out, fl
         const float f = pk_sigmoidf(gates[1][t]);
         const float u = pk_tanhf(gates[2][t]);
         const float o = pk_sigmoidf(gates[3][t]);
-        const float cj = f * c[j] + i * u;
+        const float cj = f * cold + i * u;
         c[j] = cj;
         h_out[j] = o * pk_tanhf(cj);
     }
@@ -180,17 +235,25 @@ __global__ __launch_bounds__(64) void joint_kernel(float *__restrict__ logit, co
     __shared__ __attribute__((aligned(16))) int8_t q[64 * KU];
     const int lane = threadIdx.x;
     const uint32_t p = blockIdx.x;
-    auto z4 = [&](uint32_t i) {
-        const float4 a = row4<AL>(f, i, J), g = row4<AL>(gp, i, J);
-        return make_float4(relu_sum(a.x, g.x), relu_sum(a.y, g.y), relu_sum(a.z, g.z), relu_sum(a.w, g.w));
-    };
-    const float d = quant_row<CH>(z4, J, kr, q, lane);
+    float4 vf[CH], vg[CH];
+    load_row<CH>([&](uint32_t i) { return row4<AL>(f, i, J); }, J, lane, vf);
+    load_row<CH>([&](uint32_t i) { return row4<AL>(gp, i, J); }, J, lane, vg);
+    v4i wv[KU];
+    if constexpr (kEarly<KU>)
+        panel_load<KU>(w, wstride, p, kr, lane, wv);
+    const uint32_t r = 16 * p + (lane & 15);
+    const float wsr = ws[r], br = bias ? bias[r] : 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+        vf[c] = make_float4(relu_sum(vf[c].x, vg[c].x), relu_sum(vf[c].y, vg[c].y), relu_sum(vf[c].z, vg[c].z),
+                            relu_sum(vf[c].w, vg[c].w));
+    const float d = quant_loaded<CH>(vf, J, kr, q, lane);
     __syncthreads();
-    const int s = panel_dot<KU>(w, wstride, p, kr, q, lane);
-    if (lane < 16) {
-        const uint32_t r = 16 * p + lane;
-        logit[r] = gemv_out(s, d, ws[r], bias, r);
-    }
+    if constexpr (!kEarly<KU>)
+        panel_load<KU>(w, wstride, p, kr, lane, wv);
+    const int s = panel_sum<KU>(wv, kr, q, lane);
+    if (lane < 16)
+        logit[r] = gemv_out(s, d, wsr, bias, br);
 }
 
 /* core/decoder.c:90-98: the first best token of [0, V] and the first best
