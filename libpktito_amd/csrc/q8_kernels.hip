@@ -748,25 +748,46 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
     row = row < T ? row : T - 1;
     /* packed: the frames are one group, unit u at qstride u, lane-ordered */
     const int8_t *ap = PACKED ? sg.q + lane * 16 : sg.q + (size_t)row * n;
-    v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
-    uint32_t u = wave;
-    for (; u + KW < kr; u += 2 * KW) {
-        const v4i w0 = *(const v4i *)(wp + (size_t)u * ws_);
-        const v4i w1 = *(const v4i *)(wp + (size_t)(u + KW) * ws_);
-        const uint32_t k0 = u * 64 + (lane >> 4) * 16, k1 = k0 + KW * 64;
-        const v4i a0 = *(const v4i *)(ap + (PACKED ? (size_t)u * sg.qstride : (k0 < n ? k0 : 0)));
-        const v4i a1 = *(const v4i *)(ap + (PACKED ? (size_t)(u + KW) * sg.qstride : (k1 < n ? k1 : 0)));
-        acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0, a0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w1, a1, acc1, 0, 0, 0);
+    /* the epilogue's operands (wave 0's lanes of frames < T), loaded first
+     * so that they arrive with the units */
+    const uint32_t t = lane & 15, c = p * 16 + (lane >> 4) * 4;
+    float *o = sg.out + (size_t)t * sg.os + c;
+    float dt = 0.0f, wsr[4] = { 0, 0, 0, 0 }, br[4] = { 0, 0, 0, 0 }, old[4] = { 0, 0, 0, 0 };
+    if (wave == 0 && t < T) {
+        dt = sg.d[t];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            wsr[r] = g.ws[c + r];
+            if (g.bias)
+                br[r] = g.bias[c + r];
+            if (g.add)
+                old[r] = o[r];
+        }
     }
-    if (u < kr) {
-        const v4i w0 = *(const v4i *)(wp + (size_t)u * ws_);
-        const uint32_t k0 = u * 64 + (lane >> 4) * 16;
-        const v4i a0 = *(const v4i *)(ap + (PACKED ? (size_t)u * sg.qstride : (k0 < n ? k0 : 0)));
-        acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0, a0, acc0, 0, 0, 0);
+    /* the wave's units u = wave + KW i, CU of them loaded at once (every
+     * load of a batch issued before its first MFMA: one memory round trip a
+     * batch, one batch for K <= 64 CU KW inputs); two accumulators so that
+     * consecutive MFMAs do not wait on each other (exact int32 sums) */
+    constexpr int CU = 8;
+    v4i acc[2] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
+    for (uint32_t u0 = wave; u0 < kr; u0 += CU * KW) {
+        v4i wv[CU], av[CU];
+#pragma unroll
+        for (int i = 0; i < CU; i++) {
+            const uint32_t u = u0 + i * KW;
+            if (u < kr) {
+                const uint32_t k = u * 64 + (lane >> 4) * 16;
+                wv[i] = *(const v4i *)(wp + (size_t)u * ws_);
+                av[i] = *(const v4i *)(ap + (PACKED ? (size_t)u * sg.qstride : (k < n ? k : 0)));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < CU; i++)
+            if (u0 + i * KW < kr)
+                acc[i & 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[i], av[i], acc[i & 1], 0, 0, 0);
     }
     __shared__ v4i red[KW][64];
-    red[wave][lane] = acc0 + acc1;
+    red[wave][lane] = acc[0] + acc[1];
     __syncthreads();
     if (wave != 0)
         return;
@@ -774,18 +795,14 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
 #pragma unroll
     for (int w = 1; w < KW; w++)
         s += red[w][lane];
-    const uint32_t t = lane & 15;
     if (t >= T)
         return;
-    const float dt = sg.d[t];
-    const uint32_t c = p * 16 + (lane >> 4) * 4;
-    float *o = sg.out + (size_t)t * sg.os + c;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        float v = __builtin_fmaf((float)s[r], dt, 0.0f) * g.ws[c + r];
+        float v = __builtin_fmaf((float)s[r], dt, 0.0f) * wsr[r];
         if (g.bias)
-            v = v + g.bias[c + r];
-        store_out1(o + r, g.add ? o[r] + v : v);
+            v = v + br[r];
+        store_out1(o + r, g.add ? old[r] + v : v);
     }
 }
 
