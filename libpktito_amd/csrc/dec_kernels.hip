@@ -273,6 +273,8 @@ __global__ __launch_bounds__(64) void argmax_kernel(uint32_t *__restrict__ tok_d
 #pragma unroll
     for (int k = 0; k < RUN; k++)
         lv[k] = k < (int)run && a + k < n ? logit[a + k] : 0.0f;
+    /* the durations' logits, lane i the i-th (up to 64), loaded with the run */
+    const float dv = lane < (int)n_dur ? logit[V + 1 + lane] : 0.0f;
     float bv = 0.0f;
     int bi = -1;
 #pragma unroll
@@ -291,13 +293,25 @@ __global__ __launch_bounds__(64) void argmax_kernel(uint32_t *__restrict__ tok_d
             bi = oi;
         }
     }
-    if (lane == 0) {
-        const float l0 = logit[0];
-        const uint32_t best = l0 != l0 || bi < 0 ? 0u : (uint32_t)bi;
-        uint32_t bd = 0;
+    /* the scan over the durations, each compared with the best so far */
+    uint32_t bd = 0;
+    if (n_dur <= 64) {
+        float bdv = __shfl(dv, 0);
+        for (uint32_t i = 1; i < n_dur; i++) {
+            const float x = __shfl(dv, (int)i);
+            if (x > bdv) {
+                bd = i;
+                bdv = x;
+            }
+        }
+    } else if (lane == 0) {
         for (uint32_t i = 1; i < n_dur; i++)
             if (logit[V + 1 + i] > logit[V + 1 + bd])
                 bd = i;
+    }
+    if (lane == 0) {
+        const float l0 = lv[0];                  /* lane 0's run starts at token 0 */
+        const uint32_t best = l0 != l0 || bi < 0 ? 0u : (uint32_t)bi;
         tok_dur[0] = best;
         tok_dur[1] = bd;
     }
