@@ -184,6 +184,34 @@ def test_upload_rejects_overlapping_bytes(hip):
         pass
 
 
+def test_upload_from_threads_takes_one(hip):
+    """Eight threads upload the same host bytes at once: exactly one upload
+    is taken and the others are refused, so no device copy is left behind
+    unreachable; the one taken releases."""
+    import threading
+    buf = np.ones(64 * 256, np.int8)
+    sc = np.ones(64, np.float32)
+    taken, refused, errs = [], [], []
+    start = threading.Barrier(8)
+
+    def up():
+        start.wait()
+        try:
+            taken.append(hip.Q8Matrix(buf, sc))
+        except hip.PkHipError as e:
+            (refused if e.code == hip.PK_HIP_EINVAL else errs).append(e)
+
+    ts = [threading.Thread(target=up) for _ in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errs and len(taken) == 1 and len(refused) == 7
+    taken[0].release()
+    with hip.Q8Matrix(buf, sc):
+        pass
+
+
 # --------------------------------------------- the measured shapes, whole ---
 
 def test_single_product_full_size(hip):
