@@ -156,13 +156,14 @@ def test_attention(hip, torch, T, D, H, valu):
     assert np.array_equal(bits(o.cpu().numpy()), bits(want))
 
 
+@pytest.mark.parametrize("T", [37, 301])
 @pytest.mark.parametrize("valu", [0, 1])
-def test_attention_special_values(hip, torch, valu):
+def test_attention_special_values(hip, torch, valu, T):
     """Subnormal and signed-zero operands, products past the float range and
     NaNs in the queries, keys, values and positions: every chain step's one
     rounding (an MFMA step or a v_fma_f32) gives the oracle's bits, NaNs
-    compared as NaN."""
-    T, D, H = 37, 128, 2
+    compared as NaN. T = 301 takes the softmax kernel of rows over 256 keys."""
+    D, H = 128, 2
     g = synth.rng(4242)
     q, k, v = (g.standard_normal((3, T, D)) * 1.5).astype(np.float32)
     p = g.standard_normal((2 * T - 1, D)).astype(np.float32)
@@ -184,7 +185,7 @@ def test_attention_special_values(hip, torch, valu):
     want = attention(q, k, v, p, bu, bv, H)
     o = torch.full((T, D), 9.0, dtype=torch.float32, device="cuda")
     ws = torch.empty((hip.attention_workspace(T, H),), dtype=torch.uint8, device="cuda")
-    say("attention special values", valu)
+    say("attention special values", valu, T)
     was = hip.force_attention(valu)
     try:
         hip.attention_dev(o, dev(torch, q), dev(torch, k), dev(torch, v), dev(torch, p), dev(torch, bu),
