@@ -630,7 +630,8 @@ constexpr int kPVK = 64, kPVS = kPVK + 4;
 __global__ __launch_bounds__(256) void att_pv_mfma_kernel(float *__restrict__ of, const float *__restrict__ S,
                                                           const float *__restrict__ inv, uint32_t Ts,
                                                           const float *__restrict__ vf, uint32_t T, uint32_t D,
-                                                          uint32_t dk) {
+                                                          uint32_t dk, int8_t *__restrict__ qp,
+                                                          float *__restrict__ qd, uint32_t qb) {
     __shared__ __attribute__((aligned(16))) float sv[2][64][kPVS], sp[2][64][kPVS];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t h = blockIdx.z, d0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
@@ -710,11 +711,61 @@ __global__ __launch_bounds__(256) void att_pv_mfma_kernel(float *__restrict__ of
             store(b ^ 1);
         __syncthreads();
     }
+    if (!qp) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const uint32_t qi = i0 + 16 * w + 4 * (lane >> 4) + (r & 3);
-        if (qi < T)
-            of[(size_t)qi * D + h * dk + d0 + 16 * (r >> 2) + (lane & 15)] = acc[r];
+        for (int r = 0; r < 16; r++) {
+            const uint32_t qi = i0 + 16 * w + 4 * (lane >> 4) + (r & 3);
+            if (qi < T)
+                of[(size_t)qi * D + h * dk + d0 + 16 * (r >> 2) + (lane & 15)] = acc[r];
+        }
+        return;
+    }
+    /* The outputs quantized in blocks of qb (32 or 64) channels of a frame,
+     * as a quantize of them would (core/encoder.c:344-346), straight into
+     * the output projection's packed activations and scales. Register r of
+     * lane l is frame 4 (l / 16) + r % 4 of the wave's 16, channel 16 (r /
+     * 4) + l % 16 of the tile's 64: a block is one or two register groups
+     * r / 4 over the 16 lanes of a DPP row. The tile's four units (16
+     * frames x 64 channels each) are put together in LDS and leave as
+     * 16-byte stores. */
+    const uint32_t c0 = h * dk + d0, G = (T + 15) / 16, NB = D / qb;
+    int8_t *unit = (int8_t *)&sp[0][0][0];             /* 4 KB, free after the loop */
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) {
+        const uint32_t t = i0 + 16 * w + 4 * (lane >> 4) + s4;
+#pragma unroll
+        for (int bk = 0; bk < 2; bk++) {
+            /* blocks of 64: one block of register groups 0..3 (bk 0 only);
+             * blocks of 32: block bk of groups 2 bk, 2 bk + 1 */
+            if (qb == 64 && bk == 1)
+                continue;
+            const int g0 = qb == 64 ? 0 : 2 * bk, ng = qb == 64 ? 4 : 2;
+            int m = 0;
+#pragma unroll
+            for (int gi = 0; gi < 4; gi++)
+                if (gi < ng)
+                    m = max(m, mag_bits(acc[4 * (g0 + gi) + s4]));
+            bool zero;
+            float dv, id;
+            block_scales((uint32_t)group_max_nonneg<16>(m), zero, dv, id);
+#pragma unroll
+            for (int gi = 0; gi < 4; gi++)
+                if (gi < ng) {
+                    const int gr = g0 + gi;
+                    unit[(16 * w + 4 * (lane >> 4) + s4) / 16 * kUnitBytes +
+                         in_unit(16 * gr + (lane & 15), (4 * (lane >> 4) + s4) & 15)] =
+                        (int8_t)(zero ? 0 : q1(acc[4 * gr + s4], id));
+                }
+            if (t < T && (lane & 15) == 0)
+                qd[(size_t)t * NB + (c0 + 16 * g0) / qb] = dv;
+        }
+    }
+    __syncthreads();
+    {
+        const uint32_t gt = tid / 64, g = i0 / 16 + gt;   /* unit gt of the tile: frames 16 gt .. */
+        if (g < G)
+            *(v4i *)(qp + ((size_t)(c0 / 64) * G + g) * kUnitBytes + 16 * (tid & 63)) =
+                *(const v4i *)(unit + gt * kUnitBytes + 16 * (tid & 63));
     }
 }
 
@@ -875,11 +926,14 @@ size_t att_workspace_floats(uint32_t T, uint32_t H) {
 }
 
 int launch_attention(float *of, float *ws, const float *qf, const float *kf, const float *vf, const float *pf,
-                     const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s) {
+                     const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s,
+                     int8_t *qp, float *qd, uint32_t qb) {
     if (T == 0)
         return 0;
     if (H == 0 || D % H || (D / H) % 64 || (uint64_t)T * att_score_stride(T) >= (1ull << 32) - 1)
         return -2;
+    if (qp && (g_att_valu || !(qb == 32 || qb == 64)))
+        return -2;                                  /* no quantizing epilogue there: nothing launched */
     const uint32_t dk = D / H, Ts = att_score_stride(T), tiles = (T + kAT - 1) / kAT, rows = H * T;
     float *S = ws, *inv = ws + (size_t)rows * Ts;
     if (g_att_valu) {
@@ -899,7 +953,8 @@ int launch_attention(float *of, float *ws, const float *qf, const float *kf, con
     if (g_att_valu)
         att_pv_kernel<<<dim3(dk / kPD, (T + kPI - 1) / kPI, H), 128, 0, s>>>(of, S, inv, Ts, vf, T, D, dk);
     else
-        att_pv_mfma_kernel<<<dim3((T + 63) / 64, dk / 64, H), 256, 0, s>>>(of, S, inv, Ts, vf, T, D, dk);
+        att_pv_mfma_kernel<<<dim3((T + 63) / 64, dk / 64, H), 256, 0, s>>>(of, S, inv, Ts, vf, T, D, dk, qp, qd,
+                                                                            qb);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

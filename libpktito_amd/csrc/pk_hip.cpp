@@ -1051,10 +1051,19 @@ int pk_hip_layer_dev(const pk_hip_layer *L, float *x, uint32_t T, const int8_t *
         if ((e = pk_hip_gemm_q8_batch_dev(jobs, 4, 0, stream)))
             return e;
     }
-    PK_LAUNCH(pkq8::launch_attention(w.of, w.S, w.qf, w.kf, w.vf, w.pf, L->bias_u, L->bias_v, T, D, L->H, s),
-              "layer attention launch");
-    PK_LAUNCH(pkq8::launch_quantize_packed(nullptr, w.act_qp, w.act_d, w.of, D, D, qb, T, s, &name),
-              "layer quantize launch");
+    /* the attention's output quantized in the PV's epilogue; where that
+     * kernel has no such epilogue (the VALU chains), written and quantized
+     * by a pass of its own */
+    const int ra = pkq8::launch_attention(w.of, w.S, w.qf, w.kf, w.vf, w.pf, L->bias_u, L->bias_v, T, D, L->H, s,
+                                          w.act_qp, w.act_d, qb);
+    if (ra == -2) {
+        PK_LAUNCH(pkq8::launch_attention(w.of, w.S, w.qf, w.kf, w.vf, w.pf, L->bias_u, L->bias_v, T, D, L->H, s),
+                  "layer attention launch");
+        PK_LAUNCH(pkq8::launch_quantize_packed(nullptr, w.act_qp, w.act_d, w.of, D, D, qb, T, s, &name),
+                  "layer quantize launch");
+    } else if (ra) {
+        return launch_fail(ra, "layer attention launch");
+    }
     if ((e = gemm(x, D, L->o, &act, w.act_qp, 1)))
         return e;
     /* the convolution module (core/encoder.c:354-362) */

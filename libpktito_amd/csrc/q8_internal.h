@@ -112,8 +112,12 @@ int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b
  * H x T row sums' inverses, att_workspace_floats(T, H) floats. */
 uint32_t att_score_stride(uint32_t T);
 size_t att_workspace_floats(uint32_t T, uint32_t H);
+/* The attention's output into of, or with qp set (the matrix-core kernels
+ * only; -2 else), quantized in blocks of qb = 32 or 64 channels into the
+ * packed copy qp and the scales qd instead (of is not written). */
 int launch_attention(float *of, float *ws, const float *qf, const float *kf, const float *vf, const float *pf,
-                     const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s);
+                     const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s,
+                     int8_t *qp = nullptr, float *qd = nullptr, uint32_t qb = 0);
 int launch_dwq(int8_t *qp, float *d, const float *u, uint32_t T, uint32_t D, const float *w, const float *b,
                uint32_t K, uint32_t qb, hipStream_t s);
 

@@ -222,9 +222,17 @@ def run_layer(hip, torch, D, H, F, K, T, qb, seed, threads=16):
     assert np.array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("valu", [0, 1])
 @pytest.mark.parametrize("T,qb", [(1, 32), (2, 64), (37, 32), (100, 64)])
-def test_layer_small(hip, torch, T, qb):
-    run_layer(hip, torch, 128, 2, 256, 9, T, qb, seed=T * 3 + qb)
+def test_layer_small(hip, torch, T, qb, valu):
+    """valu 0: the attention's output quantized in the PV's epilogue; valu 1:
+    the VALU attention, its output written and quantized by a pass of its
+    own."""
+    was = hip.force_attention(valu)
+    try:
+        run_layer(hip, torch, 128, 2, 256, 9, T, qb, seed=T * 3 + qb)
+    finally:
+        hip.force_attention(was)
 
 
 @pytest.mark.parametrize("T,qb", [(64, 32), (150, 64)])
