@@ -112,6 +112,28 @@ def test_joint(hip, torch, model):
         dd.release()
 
 
+@pytest.mark.parametrize("n_dur", [64, 70])
+def test_joint_many_durations(hip, torch, n_dur):
+    """Up to 64 durations the argmax scans them from registers (a lane
+    each); past 64 from memory: both against the oracle's joint."""
+    dec = synth.decoder_weights(synth.rng(17 + n_dur), P=64, L=2, J=64, V=40, n_dur=n_dur)
+    dw = ol.DecoderWeights(dec)
+    dd = hip.DeviceDecoder(dec, torch)
+    try:
+        g = synth.rng(19)
+        for i in range(4):
+            f, gp = (g.standard_normal((2, dec["J"])) * (1 + i)).astype(np.float32)
+            logit, tok, dur = ol.joint(dw, f, gp)
+            dd.gp.copy_(dev(torch, gp))
+            say("joint durations", n_dur, i)
+            dd.joint(dev(torch, f))
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(dd.logit.cpu().numpy()), bits(logit)), i
+            assert tuple(dd.tok_dur.cpu().numpy().tolist()) == (tok, dur), i
+    finally:
+        dd.release()
+
+
 def test_argmax_rule(hip, torch):
     """Logits placed through the bias of a zero joint matrix: ties go to the
     first, +0 and -0 are equal, a NaN never wins but at index 0, where
