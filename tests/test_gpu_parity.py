@@ -238,10 +238,13 @@ def test_single_product_full_size(hip):
 
 
 @pytest.mark.parametrize("M", [1, 4, 16])
-@pytest.mark.parametrize("K,N,real", [(1024, 4096, 4096), (4096, 1024, 1024), (640, 1040, 1030)])
+@pytest.mark.parametrize("K,N,real", [(1024, 4096, 4096), (4096, 1024, 1024), (640, 1040, 1030), (16384, 64, 64),
+                                      (4160, 32, 32)])
 def test_skinny_shapes(hip, M, K, N, real):
     """Streaming shapes: M <= 16 rows. The joint's 1030 outputs are padded to
-    1040 with zero rows and zero scales, as the model file pads them."""
+    1040 with zero rows and zero scales, as the model file pads them. K =
+    16384 gives each wave several batches of units; 4160 a last batch the
+    waves share unevenly."""
     g = synth.rng(M * 7 + K)
     wr = synth.weights(g, N, K)
     ws = synth.scales(g, N)
