@@ -109,7 +109,8 @@ def test_siluq(hip, torch, T, n, qb):
 
 
 @pytest.mark.parametrize("T,D,K,qb", [(1, 64, 9, 32), (2, 128, 9, 64), (9, 128, 9, 32), (17, 1024, 9, 32),
-                                      (100, 256, 31, 64), (750, 1024, 9, 64), (40, 128, 4, 32), (5, 64, 1, 64)])
+                                      (100, 256, 31, 64), (750, 1024, 9, 64), (40, 128, 4, 32), (5, 64, 1, 64),
+                                      (50, 128, 33, 32)])
 def test_dwq(hip, torch, T, D, K, qb):
     """GLU, the depthwise convolution with its bias and SiLU, and the blocks'
     quantize, against the oracle's glu, dwconv and quantize."""
