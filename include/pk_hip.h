@@ -83,7 +83,9 @@ int pk_hip_init(void);
  * the step a GPU backend adds after core/model.c's load_file (:783-811). The
  * host bytes and scales must not change while the matrix is uploaded (a
  * model's are its mapped file's): gemm_q8 reads the device copies, the
- * scales too when its ws is the uploaded s at that panel. */
+ * scales too when its ws is the uploaded s at that panel. A range that
+ * shares any byte with an uploaded matrix's is refused (PK_HIP_EINVAL),
+ * also when two threads upload it at once: one of them is taken. */
 int pk_hip_upload_q8(const int8_t *q, const float *s, uint32_t rows, uint32_t cols);
 
 /* Frees the device copy of the matrix whose host bytes start at q
