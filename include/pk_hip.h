@@ -301,12 +301,14 @@ int pk_hip_joint_dev(float *logit, uint32_t *tok_dur, const pk_hip_q8 *jout, con
  * tests. */
 const char *pk_hip_last_kernel(void);
 
-/* Tests and tuning: the number of tilings of the per-column product, and
- * forcing one of them for every later launch in the process (-1 restores
- * the automatic choice); returns the index forced before. Not thread-safe
- * against launches in flight on other threads. Every tiling computes the
- * same bits. */
+/* Tests and tuning: the number of tilings of the per-column product, each
+ * one's name (the name pk_hip_last_kernel gives its launches; "" past the
+ * last), and forcing one of them for every later launch in the process (-1
+ * restores the automatic choice); returns the index forced before. Not
+ * thread-safe against launches in flight on other threads. Every tiling
+ * computes the same bits. */
 int pk_hip_tilings(void);
+const char *pk_hip_tiling_name(int index);
 int pk_hip_force_tiling(int index);
 
 /* Tests and tuning: forcing the packed quantize's kernel for every later

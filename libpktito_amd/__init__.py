@@ -82,6 +82,7 @@ _SIGS = {
     "pk_hip_last_kernel": (ctypes.c_char_p, []),
     "pk_hip_tilings": (ctypes.c_int, []),
     "pk_hip_force_tiling": (ctypes.c_int, [ctypes.c_int]),
+    "pk_hip_tiling_name": (ctypes.c_char_p, [ctypes.c_int]),
     "pk_hip_force_quantize": (ctypes.c_int, [ctypes.c_int]),
     "pk_hip_force_attention": (ctypes.c_int, [ctypes.c_int]),
     "pk_hip_init": (ctypes.c_int, []),
@@ -175,6 +176,19 @@ def last_kernel():
 def tilings():
     """How many tilings the per-column product has (pk_hip_tilings)."""
     return lib().pk_hip_tilings()
+
+
+def tiling_name(index):
+    """The name of tiling `index` (pk_hip_tiling_name)."""
+    return lib().pk_hip_tiling_name(index).decode()
+
+
+def tiling_index(name):
+    """The index of the tiling called `name`, or -1."""
+    for i in range(tilings()):
+        if tiling_name(i) == name:
+            return i
+    return -1
 
 
 def force_tiling(index):

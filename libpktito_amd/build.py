@@ -2,10 +2,11 @@
 
     python -m libpktito_amd.build        (or libpktito_amd.build.build())
 
-One hipcc line for gfx950: the kernels (csrc/q8_kernels.hip, the quantizer,
-repack and products; csrc/layer_kernels.hip, the device-resident layer's
-float kernels; csrc/dec_kernels.hip, the decoder's fused per-token launches)
-and the runtime (csrc/pk_hip.cpp). The flags are part of the path's contract:
+hipcc for gfx950, each source compiled apart (in parallel) and linked into one
+shared library: the kernels (csrc/q8_kernels.hip, the quantizer, repack and
+products; csrc/layer_kernels.hip, the device-resident layer's float kernels;
+csrc/dec_kernels.hip, the decoder's fused per-token launches) and the runtime
+(csrc/pk_hip.cpp). The flags are part of the path's contract:
   -ffp-contract=off    no multiply and add the code writes apart is fused: the
                        epilogue's operations are the reference's, one rounding
                        each (its Makefile builds with the same flag);
@@ -39,16 +40,31 @@ FLAGS = [
     "-mllvm", "--amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-result",
 ]
+def flags_for(src):
+    """hipcc flags (without -shared) for one source of the library."""
+    return [x for x in FLAGS if x != "-shared"]
 
 
-def build(verbose=False):
-    """Compile libpkhip.so; raises CalledProcessError with hipcc's output on failure."""
-    cmd = [HIPCC] + FLAGS + ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc")]
-    cmd += SOURCES + ["-o", LIB + ".tmp"]
+def _run(cmd):
     r = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
         raise subprocess.CalledProcessError(r.returncode, cmd, output=out)
+    return out
+
+
+def build(verbose=False):
+    """Compile libpkhip.so; raises CalledProcessError with hipcc's output on failure."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc")]
+    with tempfile.TemporaryDirectory(prefix="pkhip-") as tmp:
+        objs = [os.path.join(tmp, os.path.basename(src) + ".o") for src in SOURCES]
+        cmds = [[HIPCC] + flags_for(src) + inc + ["-c", src, "-o", obj] for src, obj in zip(SOURCES, objs)]
+        with ThreadPoolExecutor(min(len(cmds), max(1, os.cpu_count() or 1))) as pool:
+            outs = list(pool.map(_run, cmds))
+        outs.append(_run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"] + objs + ["-o", LIB + ".tmp"]))
+    out = "\n".join(o for o in outs if o.strip())
     if verbose and out.strip():
         print(out)
     os.replace(LIB + ".tmp", LIB)

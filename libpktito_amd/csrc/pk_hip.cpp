@@ -437,6 +437,8 @@ const char *pk_hip_last_kernel(void) { return g_kernel; }
 
 int pk_hip_tilings(void) { return pkq8::ring_count(); }
 
+const char *pk_hip_tiling_name(int index) { return pkq8::ring_name(index); }
+
 int pk_hip_force_tiling(int index) { return pkq8::set_ring(index); }
 
 int pk_hip_force_quantize(int kind) { return pkq8::set_quant_kernel(kind); }

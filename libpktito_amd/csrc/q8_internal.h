@@ -89,6 +89,7 @@ int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size
 /* The pipelined product's tilings: how many, and forcing one (-1: the
  * heuristic); returns the one forced before. */
 int ring_count();
+const char *ring_name(int i);
 int set_ring(int i);
 
 /* The packed quantize's kernel: 0 one wave a column (a wave a 1024-input

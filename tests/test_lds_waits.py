@@ -46,16 +46,21 @@ def test_analysis_follows_loops_and_joins():
     assert lds_waits.violations(ok) == []
 
 
-@pytest.fixture(scope="module")
-def kernels_asm(tmp_path_factory):
+def _asm(tmp_path_factory, src):
     from libpktito_amd import build
-    out = tmp_path_factory.mktemp("asm") / "q8_kernels.s"
-    flags = [f for f in build.FLAGS if f not in ("-fPIC", "-shared")]
-    cmd = [build.HIPCC] + flags + ["--cuda-device-only", "-S", build.SOURCES[0], "-o", str(out),
-                                   "-I", os.path.join(ROOT, "include")]
+    out = tmp_path_factory.mktemp("asm") / (os.path.basename(src) + ".s")
+    cmd = [build.HIPCC] + build.flags_for(src) + ["--cuda-device-only", "-S", src, "-o", str(out),
+                                                  "-I", os.path.join(ROOT, "include"),
+                                                  "-I", os.path.dirname(src)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-2000:]
     return out.read_text()
+
+
+@pytest.fixture(scope="module")
+def kernels_asm(tmp_path_factory):
+    from libpktito_amd import build
+    return _asm(tmp_path_factory, next(s for s in build.SOURCES if s.endswith("q8_kernels.hip")))
 
 
 def test_product_kernels_wait_before_touching_lds_reads(kernels_asm):
