@@ -89,7 +89,10 @@ int pk_hip_init(void);
 int pk_hip_upload_q8(const int8_t *q, const float *s, uint32_t rows, uint32_t cols);
 
 /* Frees the device copy of the matrix whose host bytes start at q
- * (core/model.c:868-883's pk_model_free gains this call); all of them. */
+ * (core/model.c:868-883's pk_model_free gains this call); all of them.
+ * These wait for host-pointer products (pk_hip_gemm_q8) in flight on other
+ * threads; the device-resident entries below are asynchronous, so their
+ * caller must not release a matrix while products on it are queued. */
 int pk_hip_release_q8(const int8_t *q);
 void pk_hip_release_all(void);
 
@@ -101,10 +104,14 @@ void pk_hip_release_all(void);
 int pk_hip_quantize(pk_hip_act *a, const float *x, size_t xs);
 
 /* The table's gemm_q8 (backend/kernels.h:60-78, :257-258), on host pointers:
- * out[t * os + r] for r < rows, t < a->T, with w pointing at a whole panel of
- * an uploaded matrix and ws, bias its scales and bias from that panel on.
- * The floats between one column's outputs and the next are not touched.
- * Any of the four IEEE rounding modes the calling thread has set. */
+ * out[t * os + r] for r < rows, t < a->T, w the PK_Q8 panels of those rows
+ * and ws, bias their scales and biases. Where w is a whole panel of an
+ * uploaded matrix the device copy is used; any other w (a caller's own
+ * buffer, as the reference's checkers pass) is copied to the device and
+ * repacked for this call alone: slower, the same bits. The floats between
+ * one column's outputs and the next are not touched. Any of the four IEEE
+ * rounding modes the calling thread has set. A release of the matrix
+ * waits until the call has returned. */
 int pk_hip_gemm_q8(float *out, size_t os, const int8_t *w, const float *ws, const float *bias,
                    uint32_t rows, const pk_hip_act *a, int add);
 

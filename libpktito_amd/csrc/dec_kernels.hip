@@ -354,7 +354,7 @@ int launch_gemv(float *out, const int8_t *w, uint64_t wstride, const float *ws, 
     const bool al = n % 4 == 0 && al16(x);
     PK_DEC_SIZE(n, kr, al,
                 (gemv_kernel<CH, KU, AL><<<rows / 16, 64, 0, s>>>(out, w, wstride, ws, bias, x, n, kr, add)));
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_lstm(float *h_out, float *c, const float *h_in, const float *x, const int8_t *wx, const float *wxs,
@@ -366,7 +366,7 @@ int launch_lstm(float *h_out, float *c, const float *h_in, const float *x, const
     PK_DEC_SIZE(P, kr, al,
                 (lstm_kernel<CH, KU, AL><<<P / 16, 256, 0, s>>>(h_out, c, h_in, x, wx, wxs, wh, whs, wstride, b, P,
                                                                 kr)));
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstride, const float *ws,
@@ -382,7 +382,7 @@ int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstr
         argmax_kernel<32><<<1, 64, 0, s>>>(tok_dur, logit, V, n_dur);
     else
         argmax_kernel<64><<<1, 64, 0, s>>>(tok_dur, logit, V, n_dur);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 }  // namespace pkq8

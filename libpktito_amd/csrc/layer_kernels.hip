@@ -892,7 +892,7 @@ int launch_normq(int8_t *qp, float *d, const float *x, uint32_t n, uint32_t T, c
         if (small) PK_NQ(4, 64); else PK_NQ(16, 64);
     }
 #undef PK_NQ
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b, float eps, hipStream_t s) {
@@ -904,7 +904,7 @@ int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b
         norm_kernel<4><<<(T + 3) / 4, 256, 0, s>>>(x, n, T, w, b, eps);
     else
         norm_kernel<16><<<(T + 3) / 4, 256, 0, s>>>(x, n, T, w, b, eps);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 /* The attention's kernels: 0 the matrix cores' (the default), 1 the VALU
@@ -955,7 +955,7 @@ int launch_attention(float *of, float *ws, const float *qf, const float *kf, con
     else
         att_pv_mfma_kernel<<<dim3((T + 63) / 64, dk / 64, H), 256, 0, s>>>(of, S, inv, Ts, vf, T, D, dk, qp, qd,
                                                                             qb);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_dwq(int8_t *qp, float *d, const float *u, uint32_t T, uint32_t D, const float *w, const float *b,
@@ -969,7 +969,7 @@ int launch_dwq(int8_t *qp, float *d, const float *u, uint32_t T, uint32_t D, con
         dwq_kernel<32><<<grid, 256, 0, s>>>(qp, d, u, T, D, w, b, K);
     else
         dwq_kernel<64><<<grid, 256, 0, s>>>(qp, d, u, T, D, w, b, K);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 }  // namespace pkq8

@@ -51,10 +51,14 @@ int hip_fail(hipError_t e, const char *what) {
 
 /* A launcher's nonzero return: -2 sizes no kernel takes (nothing launched),
  * otherwise the HIP error the launch left. */
+/* A launcher's failure: -2 the sizes fit no kernel; else the launch's own
+ * error, which the launchers leave set (they peek at it) and this reads
+ * and clears. */
 int launch_fail(int r, const char *what) {
     if (r == -2)
         return fail(PK_HIP_EINVAL, "%s: the sizes fit no kernel", what);
-    return hip_fail(hipGetLastError(), what);
+    const hipError_t e = hipGetLastError();
+    return hip_fail(e == hipSuccess ? hipErrorLaunchFailure : e, what);
 }
 
 #define PK_TRY(call)                                          \
@@ -574,31 +578,40 @@ int pk_hip_gemm_q8(float *out, size_t os, const int8_t *w, const float *ws, cons
         return PK_HIP_OK;          /* no columns: nothing read, nothing written */
     if (!out || !w || !ws)
         return fail(PK_HIP_EINVAL, "gemm_q8: out, w or ws is NULL");
+    if (rows % 16)
+        return fail(PK_HIP_EINVAL, "gemm_q8: rows %u is not a multiple of 16", rows);
     if (a->T > 1 && os < rows)
         return fail(PK_HIP_EINVAL, "gemm_q8: output stride %zu is under rows %u", os, rows);
     const int rmode = rmode_of_host();
     if (rmode < 0)
         return fail(PK_HIP_EROUND, "gemm_q8: unknown rounding mode");
-    const pk_hip_q8 *m;
-    uint32_t r0;
-    {
-        std::shared_lock<std::shared_mutex> lk(g_reg_mu);
-        m = holding(w);
-        if (!m)
-            return fail(PK_HIP_ENOTUP, "gemm_q8: w %p is inside no uploaded matrix", (const void *)w);
+    /* The registry stays locked (shared) until the call has returned its
+     * outputs, so that a release of the matrix waits for it. */
+    std::shared_lock<std::shared_mutex> lk(g_reg_mu);
+    const pk_hip_q8 *m = holding(w);
+    uint32_t r0 = 0;
+    if (m) {
         const size_t off = (size_t)(w - m->hq), panel = (size_t)16 * m->cols;
         if (off % panel)
             return fail(PK_HIP_EINVAL, "gemm_q8: w is not at a panel of its matrix");
         r0 = (uint32_t)(off / panel) * 16;
+        if ((e = check_panel(m, r0, rows, a->n)))
+            return e;
+    } else if (a->n > 16384) {
+        return fail(PK_HIP_EINVAL, "gemm_q8: n %u over 16384", a->n);
     }
-    if ((e = check_panel(m, r0, rows, a->n)))
-        return e;
     Lease l;
     if ((e = lease(l)))
         return e;
     const size_t n = a->n, T = a->T, nb = n / a->qb, R = rows;
     const size_t bq = up256(T * n), bd = up256(T * nb * 4), bw = up256(R * 4), bo = up256(T * R * 4);
-    if ((e = reserve(l.c, bq + bd + 2 * bw + bo)))
+    /* Weights inside no uploaded matrix (a caller's own buffer, as the
+     * reference's checkers pass) are staged for this call alone: their
+     * PK_Q8 bytes copied and repacked into the lease's device memory, then
+     * the same kernels run. Slower (a copy and a repack a call), same bits. */
+    const uint32_t ku = pkq8::units_per_panel(a->n);
+    const size_t braw = m ? 0 : up256(R * n), bunits = m ? 0 : up256(R / 16 * ku * (size_t)pkq8::kUnitBytes);
+    if ((e = reserve(l.c, bq + bd + 2 * bw + bo + braw + bunits)))
         return e;
     char *p = l.c->dev;
     int8_t *dq = (int8_t *)p;
@@ -607,12 +620,28 @@ int pk_hip_gemm_q8(float *out, size_t os, const int8_t *w, const float *ws, cons
     float *db = (float *)(p + bq + bd + bw);
     float *dout = (float *)(p + bq + bd + 2 * bw);
     hipStream_t s = l.c->stream;
+    pk_hip_q8 staged;
+    if (!m) {
+        int8_t *draw = (int8_t *)(p + bq + bd + 2 * bw + bo);
+        staged.hq = w;
+        staged.hs = nullptr;
+        staged.rows = rows;
+        staged.cols = a->n;
+        staged.ku = ku;
+        staged.w = (int8_t *)(p + bq + bd + 2 * bw + bo + braw);
+        staged.s = nullptr;
+        if ((e = h2d(l.c, draw, w, R * n, 1, 0)))
+            return e;
+        if (pkq8::launch_repack(staged.w, draw, rows, a->n, s))
+            return launch_fail(-1, "repack launch");
+        m = &staged;
+    }
     if ((e = h2d(l.c, dq, a->q, T * n, 1, 0)) || (e = h2d(l.c, dd, a->d, T * nb * 4, 1, 0)))
         return e;
     /* the scales a model binds are the uploaded matrix's own, already on the
      * device; other scales are copied */
-    const float *wsd = m->s + r0;
-    if (ws != m->hs + r0) {
+    const float *wsd = m->s ? m->s + r0 : nullptr;
+    if (!m->hs || ws != m->hs + r0) {
         if ((e = h2d(l.c, dws, ws, R * 4, 1, 0)))
             return e;
         wsd = dws;

@@ -375,7 +375,7 @@ static int launch_quantize_packed_op(int8_t *q, int8_t *qp, float *d, const floa
         if (small) PK_QP(4, 64, "<4,qb64>"); else PK_QP(16, 64, "<16,qb64>");
     }
 #undef PK_QP
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,
@@ -433,7 +433,7 @@ int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, 
         }
         }
     }
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 /* -------------------------------------------------------------- repack --
@@ -468,7 +468,7 @@ int launch_repack(int8_t *dst, const int8_t *src, uint32_t rows, uint32_t cols, 
     if (slots == 0)
         return 0;
     repack_kernel<<<(uint32_t)((slots + 255) / 256), 256, 0, s>>>(dst, src, panels, cols, ku);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 /* ------------------------------------------------------------- product --
@@ -1781,13 +1781,13 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
                 gemm_q8_skinny_kernel<4, false><<<panels, 256, 0, s>>>(g, tab.s[0]);
             *name = packed ? "skinny_packed<4>" : "skinny<4>";
         }
-        return hipGetLastError() == hipSuccess ? 0 : -1;
+        return hipPeekAtLastError() == hipSuccess ? 0 : -1;
     }
     if (mode == 0) {
         const int c = pick_ring(g.rows, frames, g.ku);
         kRing[c].run(g, tab, s);
         *name = kRing[c].name;
-        return hipGetLastError() == hipSuccess ? 0 : -1;
+        return hipPeekAtLastError() == hipSuccess ? 0 : -1;
     }
     /* blocks of 64 or 32 inputs (the encoder's modes): the pipelined tile
      * the heuristic picks for these frames, if it has a blocked variant */
@@ -1807,7 +1807,7 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
             run(g, tab, s);
             snprintf(buf, sizeof buf, "%s %s%s", kRing[c].name, modes[mode], g.oqp ? " silu-quantized" : "");
             *name = buf;
-            return hipGetLastError() == hipSuccess ? 0 : -1;
+            return hipPeekAtLastError() == hipSuccess ? 0 : -1;
         }
     }
     if (g.oqp)
@@ -1822,7 +1822,7 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
         snprintf(buf, sizeof buf, "tiled<64x64> %s", modes[mode]);
     }
     *name = buf;
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_gemm_batch(const JobTable &jobs, hipStream_t s, const char **name) {
@@ -1846,7 +1846,7 @@ int launch_gemm_batch(const JobTable &jobs, hipStream_t s, const char **name) {
         static const char *const modes[] = { "", " blocks of 64k", " blocks of 32k" };
         snprintf(buf, sizeof buf, "%s%s", kRing[c].name, modes[mode]);
         *name = buf;
-        return hipGetLastError() == hipSuccess ? 0 : -1;
+        return hipPeekAtLastError() == hipSuccess ? 0 : -1;
     }
     /* inputs too short for the pipelined tile: one launch a job */
     for (uint32_t j = 0; j < jobs.njobs; j++) {

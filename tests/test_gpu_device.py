@@ -256,17 +256,18 @@ def test_batch_of_products(hip, torch, K, qb):
             m.release()
 
 
-@pytest.mark.parametrize("qb", [32, 64])
-@pytest.mark.parametrize("M,K,N", [(750, 1024, 1024), (300, 4096, 1024), (37, 1056, 208), (129, 512, 64),
-                                   (1499, 1024, 96)])
+BLOCKED = [(qb, M, K, N) for (M, K, N) in [(750, 1024, 1024), (300, 4096, 1024), (37, 1056, 208), (129, 512, 64),
+                                           (1499, 1024, 96)]
+           for qb in (32, 64) if K % qb == 0]
+
+
+@pytest.mark.parametrize("qb,M,K,N", BLOCKED)
 def test_blocked_products(hip, torch, qb, M, K, N):
     """The encoder's blocks (qb 32 and 64) on the pipelined tiles: the packed
     quantize's q, d and packed bytes are the oracle's, and the product of every
     tiling with a blocked variant, packed and row-major, with bias and add,
     under each rounding mode, is the oracle's, bit for bit. K = 1056 has an
     odd number of 32-input blocks and a padding unit past them."""
-    if K % qb:
-        pytest.skip("qb does not divide K")
     import ctypes.util
     libm = ctypes.CDLL(ctypes.util.find_library("m"))
     g = synth.rng(M + K + N + qb)
@@ -366,3 +367,43 @@ def test_packed_quantize_kernels(hip, torch, T, n, qb):
                 assert np.array_equal(unpack_packed(qp.cpu().numpy(), n, T), q.reshape(T, n))
     finally:
         hip.force_quantize(-1)
+
+
+STRIDED = [(n, xs, qb) for (n, xs) in [(1024, 1056), (1024, 2048), (96, 128), (4096, 4128), (640, 704)]
+           for qb in (None, 32, 64) if qb is None or n % qb == 0]
+
+
+@pytest.mark.parametrize("n,xs,qb", STRIDED)
+def test_quantize_reads_columns_at_a_stride(hip, torch, n, xs, qb):
+    """quantize_dev and quantize_packed_dev with xs > n: column t's inputs at
+    x + t xs (backend/kernels.h:47-58), the floats between one column's n
+    and the next left unread, as kcheck draws xs = n + 32 (tests/kcheck.c:
+    98-118) and the chained encoder reads the first 1024 of pw1's 2048
+    outputs a row. The floats past n hold NaN and huge values, so a kernel
+    that read them would zero the block or change its scale."""
+    qbv = n if qb is None else qb
+    g = synth.rng(n * 7 + xs + qbv)
+    dev = torch.device("cuda")
+    for T in (1, 37, 750):
+        x = synth.activations(g, T, xs)
+        x[:, n:] = np.float32(np.nan)
+        x[::3, n:] = np.float32(3e38)
+        q, d = ol.quantize(x.reshape(-1), T, n, qbv, xs)
+        xt = torch.from_numpy(x).to(dev)
+        qt = torch.empty((T, n), dtype=torch.int8, device=dev)
+        dt = torch.empty((T * (n // qbv),), dtype=torch.float32, device=dev)
+        say("strided quantize", n, xs, qbv, T)
+        hip.quantize_dev(qt, dt, xt, n, qbv, T, xs)
+        torch.cuda.synchronize()
+        assert np.array_equal(qt.cpu().numpy().reshape(-1), q), (n, xs, qbv, T)
+        assert np.array_equal(bits(dt.cpu().numpy()), bits(d)), (n, xs, qbv, T)
+        if qb in (None, 32, 64) and n <= 4096:
+            qp = torch.zeros((hip.packed_bytes(n, T),), dtype=torch.int8, device=dev)
+            qt2 = torch.empty((T, n), dtype=torch.int8, device=dev)
+            dt2 = torch.empty_like(dt)
+            say("strided packed quantize", n, xs, qbv, T)
+            hip.quantize_packed_dev(qt2, qp, dt2, xt, n, T, xs, qb=qb)
+            torch.cuda.synchronize()
+            assert np.array_equal(qt2.cpu().numpy().reshape(-1), q), (n, xs, qbv, T)
+            assert np.array_equal(bits(dt2.cpu().numpy()), bits(d)), (n, xs, qbv, T)
+            assert np.array_equal(unpack_packed(qp.cpu().numpy(), n, T), q.reshape(T, n))

@@ -198,9 +198,11 @@ def test_attention_special_values(hip, torch, valu, T):
     assert np.array_equal(bits(o.cpu().numpy()), bits(want))
 
 
-def run_layer(hip, torch, D, H, F, K, T, qb, seed, threads=16):
+def run_layer(hip, torch, D, H, F, K, T, qb, seed, threads=16, tweak=None):
     g = synth.rng(seed)
     w = layer_weights(g, D=D, H=H, F=F, K=K)
+    if tweak:
+        tweak(w)
     x = g.standard_normal((T, D)).astype(np.float32)
     ape, ape_q, ape_d = positions(g, T, D, qb)
     R = 2 * T - 1
@@ -239,3 +241,35 @@ def test_layer_small(hip, torch, T, qb, valu):
 @pytest.mark.parametrize("T,qb", [(64, 32), (150, 64)])
 def test_layer_model_shapes(hip, torch, T, qb):
     run_layer(hip, torch, 1024, 8, 4096, 9, T, qb, seed=T + qb)
+
+
+@pytest.mark.parametrize("T,qb", [(750, 32)])
+def test_layer_model_shapes_at_a_minute(hip, torch, T, qb):
+    """The whole layer at the bench's size: a minute of audio (750 frames),
+    d_model 1024, 8 heads, ff 4096, 9 taps, blocks of 32: the band of
+    position rows and the 750-key softmax and PV the bench times."""
+    run_layer(hip, torch, 1024, 8, 4096, 9, T, qb, seed=T + qb)
+
+
+@pytest.mark.parametrize("valu", [0, 1])
+@pytest.mark.parametrize("qb", [32, 64])
+def test_layer_attention_output_special_values(hip, torch, valu, qb):
+    """Special values reaching the attention's output, which the output
+    projection's activations quantize (on the matrix cores in PV's epilogue,
+    valu 0; by a pass of its own after the VALU attention, valu 1): v's row
+    scales planted so that head 0's channel 5 is NaN for every frame, head
+    1's channel 70 infinite, head 2's channels 128..159 zero and head 3's
+    192..223 subnormal, their attention outputs under 2^-121. Each block
+    holding them must quantize as zeros with d = 0 (backend/ref/kernels.c:
+    24-58), and the layer's output is the oracle's bit for bit."""
+    def plant(w):
+        s = w["v_s"]
+        s[5] = np.float32(np.nan)
+        s[70] = np.float32(np.inf)
+        s[128:160] = 0.0
+        s[192:224] = np.float32(1e-44)
+    was = hip.force_attention(valu)
+    try:
+        run_layer(hip, torch, 256, 4, 512, 9, 37, qb, seed=91 + qb, tweak=plant)
+    finally:
+        hip.force_attention(was)
