@@ -245,6 +245,18 @@ int pk_hip_attention_dev(float *o, const float *q, const float *k, const float *
                          const float *bias_u, const float *bias_v, uint32_t T, uint32_t D, uint32_t H, void *ws,
                          size_t ws_bytes, void *stream);
 
+/* pk_hip_attention_dev with its scores and row sums in a static scratch
+ * array of the library (24 MiB on each GPU it runs on, held until the
+ * process ends) instead of a workspace: no allocation of any kind, for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * pk_hip_attention_workspace(T, H) must be at most 24 MiB (T up to 884 at 8
+ * heads), else PK_HIP_EINVAL. Every call on one GPU shares the array:
+ * calls that overlap on one GPU (on two streams, or two threads) race. */
+int pk_hip_attention_noalloc_dev(float *o, const float *q, const float *k, const float *v, const float *p,
+                                 const float *bias_u, const float *bias_v, uint32_t T, uint32_t D, uint32_t H,
+                                 void *stream);
+
 /* One encoder layer's weights on the device (core/model.h:45-53): the
  * eleven matrices uploaded, the vectors as device pointers. D = d_model
  * (a multiple of 64 up to 4096), H heads of D / H (a multiple of 64),

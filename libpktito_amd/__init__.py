@@ -123,6 +123,7 @@ _SIGS = {
     "pk_hip_attention_workspace": (ctypes.c_size_t, [ctypes.c_uint32, ctypes.c_uint32]),
     "pk_hip_attention_dev": (ctypes.c_int, [ctypes.c_void_p] * 7 + [ctypes.c_uint32] * 3 +
                              [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "pk_hip_attention_noalloc_dev": (ctypes.c_int, [ctypes.c_void_p] * 7 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]),
     "pk_hip_layer_workspace": (ctypes.c_size_t, [ctypes.POINTER(LayerW), ctypes.c_uint32, ctypes.c_uint32]),
     "pk_hip_gemv_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_int, ctypes.c_void_p]),
@@ -383,6 +384,13 @@ def attention_dev(o, q, k, v, p, bias_u, bias_v, T, D, H, ws, stream=None):
     ws a uint8 tensor of attention_workspace(T, H) bytes."""
     _check(lib().pk_hip_attention_dev(_dptr(o), _dptr(q), _dptr(k), _dptr(v), _dptr(p), _dptr(bias_u),
                                       _dptr(bias_v), T, D, H, _dptr(ws), ws.numel(), _stream(stream)))
+
+
+def attention_noalloc_dev(o, q, k, v, p, bias_u, bias_v, T, D, H, stream=None):
+    """attention_dev with the scores in the library's static scratch: no
+    workspace, nothing allocated (pk_hip_attention_noalloc_dev)."""
+    _check(lib().pk_hip_attention_noalloc_dev(_dptr(o), _dptr(q), _dptr(k), _dptr(v), _dptr(p), _dptr(bias_u),
+                                              _dptr(bias_v), T, D, H, _stream(stream)))
 
 
 class DeviceLayer:

@@ -16,6 +16,7 @@
 #include "q8_internal.h"
 
 #include <math.h>
+#include <mutex>
 
 #pragma clang fp contract(off)
 
@@ -918,6 +919,45 @@ int set_attention_kernels(int valu) {
 }
 
 uint32_t att_score_stride(uint32_t T) { return (T + 3) & ~3u; }
+
+/* ---------------------------------------------------- static scratch --
+ *
+ * The attention's scores and row sums for callers that cannot allocate
+ * (pk_hip_attention_noalloc_dev): a file-scope device array of
+ * kStaticScratchBytes, which every GPU the library runs on holds from the
+ * code object's load until the process ends. Host code never names the
+ * array as memory: its address on a device is taken once, with that device
+ * current (hipGetSymbolAddress), kept per device, and that address is what
+ * the kernels are given. Every call on one GPU shares its array: calls that
+ * overlap on one GPU race. */
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void *g_scratch_at[kMaxDevices];
+
+void *static_scratch(int dev, int *err) {
+    if (dev < 0 || dev >= kMaxDevices) {
+        *err = (int)hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_at[dev]) {
+        int cur = -1;
+        hipError_t e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != dev)
+            e = hipErrorInvalidDevice;      /* the caller makes dev current first */
+        void *p = nullptr;
+        if (e == hipSuccess)
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            *err = (int)(e != hipSuccess ? e : hipErrorInvalidSymbol);
+            return nullptr;
+        }
+        g_scratch_at[dev] = p;
+    }
+    *err = 0;
+    return g_scratch_at[dev];
+}
 
 size_t att_workspace_floats(uint32_t T, uint32_t H) {
     /* the scores, then each row's 1 / sum (16-byte aligned: the stride is

@@ -101,6 +101,10 @@ void init_once() {
     }
     g_dev = dev;
     g_init = PK_HIP_OK;
+    /* the static scratch's address on this device, taken once now (a
+     * failure here fails only the entry that uses it) */
+    int se = 0;
+    (void)pkq8::static_scratch(dev, &se);
 }
 
 /* ---------------------------------------------------------- registry --- */
@@ -1010,6 +1014,33 @@ int pk_hip_attention_dev(float *o, const float *q, const float *k, const float *
     if (ws_bytes < pk_hip_attention_workspace(T, H))
         return fail(PK_HIP_EINVAL, "attention_dev: workspace of %zu bytes, %zu needed", ws_bytes,
                     pk_hip_attention_workspace(T, H));
+    PK_LAUNCH(pkq8::launch_attention(o, (float *)ws, q, k, v, p, bias_u, bias_v, T, D, H, (hipStream_t)stream),
+              "attention launch");
+    g_kernel = "attention";
+    return PK_HIP_OK;
+}
+
+int pk_hip_attention_noalloc_dev(float *o, const float *q, const float *k, const float *v, const float *p,
+                                 const float *bias_u, const float *bias_v, uint32_t T, uint32_t D, uint32_t H,
+                                 void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (T == 0)
+        return PK_HIP_OK;
+    if (!o || !q || !k || !v || !p || !bias_u || !bias_v || H == 0 || D % H || (D / H) % 64)
+        return fail(PK_HIP_EINVAL, "attention_noalloc_dev: heads of a multiple of 64 dimensions, every pointer set");
+    const size_t need = pk_hip_attention_workspace(T, H);
+    if (need > pkq8::kStaticScratchBytes)
+        return fail(PK_HIP_EINVAL,
+                    "attention_noalloc_dev: %u frames of %u heads need %zu bytes of scores, over the static "
+                    "scratch's %zu", T, H, need, pkq8::kStaticScratchBytes);
+    int dev = -1;
+    PK_TRY(hipGetDevice(&dev));
+    int se = 0;
+    void *ws = pkq8::static_scratch(dev, &se);
+    if (!ws)
+        return hip_fail((hipError_t)se, "attention_noalloc_dev: the static scratch's address");
     PK_LAUNCH(pkq8::launch_attention(o, (float *)ws, q, k, v, p, bias_u, bias_v, T, D, H, (hipStream_t)stream),
               "attention launch");
     g_kernel = "attention";

@@ -119,6 +119,14 @@ size_t att_workspace_floats(uint32_t T, uint32_t H);
 int launch_attention(float *of, float *ws, const float *qf, const float *kf, const float *vf, const float *pf,
                      const float *bu, const float *bv, uint32_t T, uint32_t D, uint32_t H, hipStream_t s,
                      int8_t *qp = nullptr, float *qd = nullptr, uint32_t qb = 0);
+/* The attention's static scratch (layer_kernels.hip) for callers that
+ * cannot allocate: its bytes, and its address on device dev, which must be
+ * current (taken once a device; NULL with the HIP error in *err if it
+ * cannot be had). */
+constexpr size_t kStaticScratchBytes = (size_t)24 << 20;
+constexpr int kMaxDevices = 64;
+void *static_scratch(int dev, int *err);
+
 int launch_dwq(int8_t *qp, float *d, const float *u, uint32_t T, uint32_t D, const float *w, const float *b,
                uint32_t K, uint32_t qb, hipStream_t s);
 
