@@ -1,33 +1,36 @@
-"""The int8 product path on one MI355X: throughput of one FastConformer layer's
-int8 products, with the roofline of its dominant kernel and a CPU baseline.
+"""The int8 product path on one MI355X: encoder-GEMM milliseconds per audio
+minute over the 24-layer FastConformer encoder's int8 products at ten
+minutes of audio, with the roofline of its dominant kernel and the same
+workload on the host's cores beside it.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu]
 
-A step is one pass of the hot path over one layer at a minute of audio: the
-eleven int8 products of a FastConformer layer (d_model 1024, feed-forward
-4096, 8 heads, the convolution module's pointwise 2048) at M = 750 frames
-(2M - 1 = 1499 for the positions' projection), each input quantized per row
-to int8 and multiplied with exact int32 sums into fp32 outputs by the
-reference's epilogue. Weights, scales and fp32 inputs are synthetic (int8
-uniform [-127, 127], scales uniform [1e-3, 1e-2], N(0, 1) inputs, half-normal
-into the down projections) and resident in HBM before the timed region. The
-16 launches of a step (8 quantizes, 7 products, and one launch of the
-attention's q, k, v and positions' products, which the reference runs from
-one activation and the positional encodings) are captured once into a HIP
-graph and replayed; K replays are timed with events on the stream they run
-on.
+A step is one pass of the hot path over one batch: the 24 layers' int8
+products (each layer's q, k, v, o, the positions' projection on 2M - 1
+rows, the two feed-forward modules' 1024 -> 4096 and 4096 -> 1024, the
+convolution module's pointwise 1024 -> 2048 and 1024 -> 1024, d_model
+1024, 8 heads) at M = 7500 frames, every layer with independent weights
+(~0.6 GB of int8 resident in HBM), each product's input the previous one's
+fp32 output quantized per row to int8, multiplied with exact int32 sums into
+fp32 outputs by the reference's epilogue. Weights, scales and the first fp32
+input are synthetic (int8 uniform [-127, 127], scales uniform [1e-3, 1e-2]
+scaled so the chain stays finite, N(0, 1) frames) and resident in HBM before
+the timed region. A sweep's 385 launches (a quantize and a product each,
+q, k, v and the positions in one launch) are captured once into a HIP graph
+and replayed; K replays are timed with events on the stream they run on.
+`value` is the sweep's milliseconds over its ten minutes of audio.
 
-Printed: one JSON line. `value` is TOPS (2 M K N over the step's time). The
-`extra` object adds the same layer in the encoder's blocks of 32 and 64, the
-device-resident layer (the whole of core/encoder.c's layer in HBM: layer
-norms, SiLU and depthwise producers fused with their quantizes, the
-attention's float part and the eleven products, one pk_hip_layer_dev call)
-beside the same layer on the host's cores from the reference's own kernels,
-the long-form layer (M = 7500) and a ragged batch of 8 segments in grouped
-launches, the 24-layer chained encoder sweep in ms per audio-minute, and the
-skinny (M <= 16) shapes against HBM. `cpu_baseline` times the reference's own
-backends (compiled from its sources into oracle/_ref) on the host's cores,
-on the same inputs.
+`roofline` is the dominant kernel's (the product kernel taking the most
+time a layer), timed alone in a graph of back-to-back launches. `cpu_baseline`
+runs the same chain, on the same weights and input, with the reference's
+fastest kernels this host runs (compiled from its sources into oracle/_ref)
+over every core. The `extra` object adds the sweep's TOPS and per-product
+kernels, the sweep at one minute of audio, one layer's products at M = 750
+(per-row and in the encoder's blocks of 32 and 64), the device-resident
+layer (the whole of core/encoder.c's layer in HBM) beside the same layer on
+the host's cores, the long-form layer and a ragged batch of 8 segments in
+grouped launches, the skinny (M <= 16) shapes against HBM, the decoder's
+token steps and the host-pointer drop-in as the reference's pool deals it.
 """
 import argparse
 import ctypes
@@ -57,15 +60,21 @@ def _addr(a):
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--quick", action="store_true", help="the layer only: no extras, no CPU baseline")
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--quick", action="store_true", help="the headline sweep only: no extras, no CPU baseline")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=8.0)
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--profile-kernel", default=None,
                    help="only launch the named product's kernel 50 times (for rocprofv3 --pmc runs)")
     p.add_argument("--profile-layer", type=int, default=0, metavar="QB",
                    help="only replay the device-resident layer at M=750 in blocks of QB (for rocprofv3)")
+    p.add_argument("--profile-m", type=int, default=750, metavar="M",
+                   help="frames of --profile-kernel's product (750 or 7500)")
+    p.add_argument("--profile-sweep", type=int, default=0, metavar="M",
+                   help="only replay the 24-layer sweep at M frames --steps times (for rocprofv3)")
+    p.add_argument("--profile-skinny", default=None, metavar="M,K,N",
+                   help="only M-row products through rotated K x N matrices, 50 launches (for rocprofv3)")
     p.add_argument("--profile-decoder", action="store_true",
                    help="the decoder's token steps only (graphs of a prediction and a joint, no CPU leg)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -306,7 +315,7 @@ def encoder_sweep(pk, torch, M, seed):
     return fn, ops, layers
 
 
-def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20):
+def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20, rows=(1, 4, 16), launches=None):
     """Skinny products: M in {1, 4, 16} rows through weights rotated over more than
     512 MB of distinct matrices, so that L2 and the 256 MB MALL serve none of
     them. One graph of launches over the copies; GB/s from the algorithmic
@@ -324,12 +333,22 @@ def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20):
         for c in range(copies):
             wslice = big[c * per:(c + 1) * per]
             mats.append(pk.Q8Matrix(wslice, wsa))
-        for M in (1, 4, 16):
+        for M in rows:
             x = torch.from_numpy(synth.activations(g, M, K)).to(dev)
             q = torch.empty((M, K), dtype=torch.int8, device=dev)
             d = torch.empty((M,), dtype=torch.float32, device=dev)
             pk.quantize_dev(q, d, x, K, K, M, K)
             o = torch.empty((M, N), dtype=torch.float32, device=dev)
+
+            if launches:
+                # eager launches over the rotation, for a counter run
+                for i in range(launches):
+                    m = mats[i % len(mats)]
+                    pk.gemm_q8_dev(o, N, m, 0, N, None, None, q, d, K, K, M, 0, ws_ptr=m.dev_scales)
+                torch.cuda.synchronize()
+                out.append(dict(M=M, K=K, N=N, launches=launches, kernel=pk.last_kernel(),
+                                bytes_per_launch=N * K + 4 * N + M * K + 4 * M + 4 * M * N))
+                continue
 
             def fn():
                 for m in mats:
@@ -348,6 +367,104 @@ def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20):
 
 
 # --------------------------------------------------------- CPU baseline ---
+
+def cpu_impls():
+    """The host's kernels to time, fastest first: the reference's SIMD
+    backends this CPU can run and its scalar ref (compiled from its sources
+    into oracle/_ref), or the oracle's C restatement when that is absent.
+    Each is (kind, backend id, quantize(act, x_ptr, xs), gemm(out_ptr, os,
+    w_ptr, ws_ptr, rows, act, add)), both dealt over `cores` threads as the
+    reference's pool deals them (core/passes.c:28-46, :80-109)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+    cores = min(os.cpu_count() or 1, 64)
+    out = []
+    if ol.ref() is not None:
+        r = ol.ref()
+        for bid in ("avx512-vnni", "avx2-vnni", "ref"):
+            i = ol.ref_index(bid)
+            if i >= 0 and r.pkref_usable(i):
+                out.append(("reference", bid,
+                            lambda a, x, xs, i=i: r.pkref_quantize_threads(i, cores, ctypes.byref(a), x, xs),
+                            lambda o, os_, w, ws, rows, a, add, i=i: r.pkref_gemm_threads(
+                                i, cores, o, os_, w, ws, None, rows, ctypes.byref(a), add)))
+    if not out:
+        o = ol.oracle()
+        fq = ctypes.cast(o.pko_quantize, ctypes.c_void_p).value
+        fg = ctypes.cast(o.pko_gemm_q8, ctypes.c_void_p).value
+        out.append(("port", "oracle",
+                    lambda a, x, xs: o.pko_quantize_threads(fq, cores, ctypes.byref(a), x, xs),
+                    lambda op, os_, w, ws, rows, a, add: o.pko_gemm_threads(fg, cores, op, os_, w, ws, None, rows,
+                                                                           ctypes.byref(a), add)))
+    return cores, out
+
+
+def cpu_sweep(layers, M, seconds, impl, frames=None):
+    """The chained sweep on this host's cores: encoder_sweep's order, weights
+    and inputs (its first layer's input and the positional encodings copied
+    from the device), each product's input quantized per row from the
+    previous product's fp32 output (pw2 on the first 1024 of pw1's 2048
+    floats a frame, xs = 2048), the positions quantized once an encode. Layer
+    after layer of the chain, pass after pass over the 24, until `seconds`
+    have gone by (at least one layer), then the time a layer times 24. Every
+    step works frame by frame, so with `frames` F < M the chain runs the
+    first F frames (and 2F - 1 positions) alone and the time is per F
+    frames; ms per audio-minute is the time over F / 750 minutes."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as ol
+    kind, bid, quant, gemm = impl
+    F = M if frames is None else min(frames, M)
+    R = 2 * F - 1
+    x0 = np.ascontiguousarray(layers[0]["ff1_up"].x[:F].cpu().numpy())
+    ape = np.ascontiguousarray(layers[0]["pos"].x[:R].cpu().numpy())
+    bufs = {}
+
+    def buf(name, shape, dtype=np.float32):
+        if name not in bufs:
+            bufs[name] = np.zeros(shape, dtype)
+        return bufs[name]
+
+    def act(x, xs, K, T, tag):
+        q = buf("q" + tag, (T * K,), np.int8)
+        d = buf("d" + tag, (T,))
+        a = ol.Act(q.ctypes.data, d.ctypes.data, K, K, T)
+        quant(a, x.ctypes.data, xs)
+        return a
+
+    def run(p, a, T):
+        out = buf(p.name, (T, p.N))
+        gemm(out.ctypes.data, p.N, p.w.ctypes.data, p.ws.ctypes.data, p.N, a, p.add)
+        return out
+
+    def layers_of_the_chain():
+        """The chain's layers one by one, pass after pass over the 24."""
+        while True:
+            pa = act(ape, 1024, 1024, R, "pos")        # once an encode
+            x = x0
+            for lay in layers:
+                h = run(lay["ff1_up"], act(x, 1024, 1024, F, "a"), F)
+                fd = run(lay["ff1_down"], act(h, 4096, 4096, F, "b"), F)
+                a = act(fd, 1024, 1024, F, "a")
+                for n in ("q", "k", "v"):
+                    run(lay[n], a, F)
+                run(lay["pos"], pa, R)
+                o = run(lay["o"], act(bufs["v"], 1024, 1024, F, "a"), F)
+                p1 = run(lay["pw1"], act(o, 1024, 1024, F, "a"), F)
+                p2 = run(lay["pw2"], act(p1, 2048, 1024, F, "a"), F)
+                u = run(lay["ff2_up"], act(p2, 1024, 1024, F, "a"), F)
+                x = run(lay["ff2_down"], act(u, 4096, 4096, F, "b"), F)
+                yield
+
+    t0 = time.perf_counter()
+    done = 0
+    for _ in layers_of_the_chain():
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    el = time.perf_counter() - t0
+    return dict(kind=kind, backend=bid, ms_per_audio_minute=el / done * 24 * 1e3 / (F / 750.0), layers=done,
+                frames=F, seconds=round(el, 2))
+
 
 def cpu_baseline(prods_host, seconds):
     """The reference's backends on this host's cores, on the layer's inputs:
@@ -530,6 +647,18 @@ def recorded_traffic(kernel, M, K, N):
     return None
 
 
+def copy_calibration(torch):
+    """A plain copy of 256 MiB, three times: the known-size kernel whose
+    rocprofv3 FETCH_SIZE and WRITE_SIZE scale a product's to bytes."""
+    a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {"copied_bytes": a.numel() * 4, "times": 3}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -543,6 +672,49 @@ def cpu_model():
 
 # ------------------------------------------------------------------ main ---
 
+SWEEP_M = 7500          # ten minutes of audio in one segment
+
+
+def dominant(pk, torch, prods, launches, reps):
+    """Each product's kernel alone (kernel_ms: a graph of back-to-back
+    launches, HIP events on its stream), grouped by kernel and shape (ff1 and
+    ff2 share theirs); the group taking the most time a layer is the
+    dominant kernel. Returns (per product, the dominant group's product,
+    its kernel's name, its us a launch)."""
+    per, groups = {}, {}
+    for p in prods:
+        kms = kernel_ms(pk, torch, p, launches=launches, reps=reps)
+        kname = pk.last_kernel()
+        per[p.name] = dict(us=round(kms * 1e3, 2), kernel=kname, tops=round(p.ops() / (kms * 1e-3) / 1e12, 1),
+                           GBs=round(p.gemm_bytes() / (kms * 1e-3) / 1e9, 1),
+                           pct_mfma=round(100 * p.ops() / (kms * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS, 1))
+        key = (kname, p.M, p.K, p.N, p.add)
+        tot, _, _ = groups.get(key, (0.0, p, kms))
+        groups[key] = (tot + kms, p, kms)
+    _, dom, dkms = max(groups.values(), key=lambda t: t[0])
+    return per, dom, per[dom.name]["kernel"], dkms
+
+
+def roofline_of(dom, dname, dkms):
+    dbytes = dom.gemm_bytes()
+    intensity = dom.ops() / dbytes
+    bound = "hbm" if intensity < MFMA_INT8_PEAK_TOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
+    r = dict(bound=bound, kernel=dname, product=f"{dom.name} M={dom.M} K={dom.K} N={dom.N}",
+             unit="GB/s" if bound == "hbm" else "TFLOP/s",
+             achieved=round(dbytes / (dkms * 1e-3) / 1e9 if bound == "hbm" else dom.ops() / (dkms * 1e-3) / 1e12, 1),
+             peak=HBM_PEAK_GBS if bound == "hbm" else MFMA_INT8_PEAK_TOPS,
+             kernel_us=round(dkms * 1e3, 3), bytes_per_launch=dbytes, ops_per_launch=dom.ops(),
+             traffic=recorded_traffic(dname, dom.M, dom.K, dom.N))
+    r["frac"] = round(r["achieved"] / r["peak"], 4)
+    return r
+
+
+def release(layers):
+    for lay in layers:
+        for p in lay.values():
+            p.m.release()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -551,12 +723,7 @@ def main():
         sys.exit(2)
     import torch
     if args.copy_calibration:
-        a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
-        b = torch.empty_like(a)
-        for _ in range(3):
-            b.copy_(a)
-        torch.cuda.synchronize()
-        print(json.dumps({"copied_bytes": a.numel() * 4, "times": 3}))
+        print(json.dumps(copy_calibration(torch)))
         return
     import libpktito_amd as pk
     pk.init()
@@ -571,118 +738,159 @@ def main():
         print(json.dumps({"profiled": "device_layer", "M": M, "qb": args.profile_layer, "us_per_layer": round(us, 1),
                           "replays": args.steps}))
         return
-    prods = make_layer(pk, torch, M, seed=1)
+    if args.profile_sweep:
+        fn, _, layers = encoder_sweep(pk, torch, args.profile_sweep, seed=10 + args.profile_sweep)
+        gs = graph_of(torch, fn)
+        ms = time_graph(torch, gs, args.steps, args.warmup)
+        print(json.dumps({"profiled": "encoder_sweep", "M": args.profile_sweep, "replays": args.steps,
+                          "ms_per_sweep": round(ms, 3)}))
+        return
+    if args.profile_skinny:
+        Ms, Ks, Ns = (int(v) for v in args.profile_skinny.split(","))
+        r = skinny_rates(pk, torch, [(Ks, Ns, Ns)], rows=(Ms,), launches=50)
+        print(json.dumps({"profiled": "skinny", **r[0], "calibration": copy_calibration(torch)}))
+        return
     if args.profile_kernel:
         # the named product's kernel alone, 50 times: what the rocprofv3
         # summaries under profiles/ are cut from
+        prods = make_layer(pk, torch, args.profile_m, seed=1 if args.profile_m == 750 else 2)
         dom = next(p for p in prods if p.name == args.profile_kernel)
         for _ in range(50):
             dom.gemm(pk)
         torch.cuda.synchronize()
-        print(json.dumps({"profiled": dom.name, "kernel": pk.last_kernel(), "launches": 50,
-                          "bytes_per_launch": dom.gemm_bytes()}))
-        return
-    step = layer_step(pk, prods)
-    graph = graph_of(torch, step)
-    log("layer M=750 captured")
-    replay_ok = check_replay(pk, torch, prods, graph)
-    ms = time_graph(torch, graph, args.steps, args.warmup)
-    ops = sum(p.ops() for p in prods)
-    tops = ops / (ms * 1e-3) / 1e12
-
-    # the dominant kernel: the product whose kernel takes the most time a step
-    per = []
-    for p in prods:
-        kms = kernel_ms(pk, torch, p)
-        per.append((kms, p, pk.last_kernel()))
-    per.sort(key=lambda t: -t[0])
-    dkms, dom, dname = per[0]
-    dbytes = dom.gemm_bytes()
-    intensity = dom.ops() / dbytes
-    achieved = dbytes / (dkms * 1e-3) / 1e9
-    bound = "hbm" if intensity < MFMA_INT8_PEAK_TOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
-    roofline = dict(bound=bound, kernel=dname, product=f"{dom.name} M={dom.M} K={dom.K} N={dom.N}",
-                    unit="GB/s" if bound == "hbm" else "TFLOP/s",
-                    achieved=round(achieved if bound == "hbm" else dom.ops() / (dkms * 1e-3) / 1e12, 1),
-                    peak=HBM_PEAK_GBS if bound == "hbm" else MFMA_INT8_PEAK_TOPS,
-                    kernel_us=round(dkms * 1e3, 3), bytes_per_launch=dbytes, ops_per_launch=dom.ops(),
-                    traffic=recorded_traffic(dname, dom.M, dom.K, dom.N))
-    roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
-    per_product = {p.name: dict(us=round(k * 1e3, 2), kernel=n,
-                                tops=round(p.ops() / (k * 1e-3) / 1e12, 1),
-                                GBs=round(p.gemm_bytes() / (k * 1e-3) / 1e9, 1)) for (k, p, n) in per}
-
-    extra = dict(pct_mfma_peak=round(100 * tops / MFMA_INT8_PEAK_TOPS, 2), per_product=per_product,
-                 graph_replay_matches_eager=replay_ok,
-                 layer_quantize_bytes=sum(p.quant_bytes() for p in prods),
-                 layer_gemm_bytes=sum(p.gemm_bytes() for p in prods))
-
-    cpu = None
-    host_inputs = [(p.x_host.reshape(-1), p.w, p.ws, p.M, p.K, p.N, p.add) for p in prods]
-    log(f"layer: {ms:.4f} ms a step, {tops:.1f} TOPS; dominant {dom.name} {dkms * 1e3:.2f} us")
-    # the real encoder's blocks (qb = 32 by default, 64 in its fast mode): the
-    # same layer with blocked quantizes and products on the packed path, q, k,
-    # v and pos in one launch as in the per-row step
-    blocked = {}
-    for qb in (32, 64):
-        bd = {p.name: torch.empty((p.M * p.K // qb,), dtype=torch.float32, device=p.x.device) for p in prods}
-        src = {p.name: p for p in prods}
-        owner = {"k": "q", "v": "q"}
-        pos = src["pos"]
-        pk.quantize_packed_dev(None, pos.qp, bd["pos"], pos.x, pos.K, pos.M, pos.xs, qb=qb)  # once an encode
-
-        def blocked_step(qb=qb, bd=bd):
-            for p in prods:
-                o = src[owner.get(p.name, p.name)]
-                if p.name not in owner and p.name != "pos":
-                    pk.quantize_packed_dev(None, p.qp, bd[p.name], p.x, p.K, p.M, p.xs, qb=qb)
-                if p.name in ATTENTION:
-                    if p.name == ATTENTION[0]:
-                        group = [(a, src[owner.get(a.name, a.name)]) for a in prods if a.name in ATTENTION]
-                        pk.gemm_q8_batch_dev([(a.out, a.N, a.m, 0, a.N, a.m.dev_scales, None, ao.qp, bd[ao.name],
-                                               a.K, a.M, a.add) for a, ao in group], qb=qb)
-                    continue
-                pk.gemm_q8_packed_dev(p.out, p.N, p.m, 0, p.N, p.m.dev_scales, None, o.qp, bd[o.name], p.K, p.M,
-                                      p.add, qb=qb)
-        gb = graph_of(torch, blocked_step)
-        bms = time_graph(torch, gb, 50, 5)
-        blocked[f"qb{qb}"] = dict(ms_per_step=round(bms, 4), tops=round(ops / (bms * 1e-3) / 1e12, 1),
-                                  kernel=pk.last_kernel())
-        log(f"layer qb={qb}: {bms:.4f} ms")
-        del gb
-    extra["layer_M750_blocked"] = blocked
-
-    # the device-resident layer (the whole of core/encoder.c's layer in HBM:
-    # fused layer norm, SiLU and depthwise producers, the attention's float
-    # products, the eleven products), in the encoder's blocks
-    dlayer = {}
-    host_layer = None
-    for qb in (32, 64):
-        us, host = device_layer(pk, torch, M, qb)
-        dlayer[f"qb{qb}"] = dict(us_per_layer=round(us, 1), encoder_ms_per_audio_minute_24_layers=round(us * 24e-3, 2),
-                                 int8_product_tops=round(ops / (us * 1e-6) / 1e12, 1))
-        log(f"device layer qb={qb}: {us:.1f} us")
-        if qb == 32:
-            host_layer = host
+        kname = pk.last_kernel()
+        for p in prods:
+            p.m.release()
+        del prods
         torch.cuda.empty_cache()
-    extra["device_layer_M750"] = dlayer
+        # the known-size copy in the same process, so one counter run scales both
+        print(json.dumps({"profiled": dom.name, "M": dom.M, "kernel": kname, "launches": 50,
+                          "bytes_per_launch": dom.gemm_bytes(), "ops_per_launch": dom.ops(),
+                          "calibration": copy_calibration(torch)}))
+        return
+
+    # ---- the headline: the 24-layer chained sweep at ten minutes of audio
+    fn, sops, layers = encoder_sweep(pk, torch, SWEEP_M, seed=10 + SWEEP_M)
+    gs = graph_of(torch, fn)
+    log(f"sweep M={SWEEP_M} captured")
+    ms = time_graph(torch, gs, args.steps, args.warmup)
+    minutes = SWEEP_M / 750.0
+    value = ms / minutes
+    tops = sops / (ms * 1e-3) / 1e12
+    log(f"sweep M={SWEEP_M}: {ms:.3f} ms, {value:.4f} ms per audio-minute, {tops:.1f} TOPS")
+    del gs
+    first = [layers[0][n] for n in ("ff1_up", "ff1_down", "q", "k", "v", "pos", "o", "pw1", "pw2", "ff2_up",
+                                    "ff2_down")]
+    per_long, dom, dname, dkms = dominant(pk, torch, first, launches=8, reps=3)
+    roofline = roofline_of(dom, dname, dkms)
+    log(f"dominant {dom.name}: {dkms * 1e3:.2f} us ({dname})")
+    extra = dict(sweep_M7500=dict(ms_per_sweep=round(ms, 3), tops=round(tops, 1),
+                                  pct_mfma_peak=round(100 * tops / MFMA_INT8_PEAK_TOPS, 2), ops_per_sweep=sops,
+                                  per_product_first_layer=per_long))
+    cpu = None
+    if not args.no_cpu and not args.quick:
+        cores, impls = cpu_impls()
+        cpu = cpu_sweep(layers, SWEEP_M, args.cpu_seconds, impls[0])
+        cpu["cores"] = cores
+        log(f"cpu sweep: {cpu}")
+        scalar = [i for i in impls[1:] if i[1] == "ref"]
+        if scalar:
+            r = cpu_sweep(layers, SWEEP_M, args.cpu_seconds / 2, scalar[0], frames=750)
+            r["cores"] = cores
+            extra["cpu_ref_scalar_sweep"] = r
+    release(layers)
+    del layers, fn
+    torch.cuda.empty_cache()
 
     if not args.quick:
+        # the same sweep at one minute of audio
+        fn, sops750, layers = encoder_sweep(pk, torch, M, seed=10 + M)
+        gs = graph_of(torch, fn)
+        sms = time_graph(torch, gs, 20, 3)
+        log(f"sweep M={M}: {sms:.3f} ms")
+        extra["sweep_M750"] = dict(ms_per_sweep=round(sms, 3), ms_per_audio_minute=round(sms, 4),
+                                   tops=round(sops750 / (sms * 1e-3) / 1e12, 1),
+                                   pct_mfma_peak=round(100 * sops750 / (sms * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS, 2))
+        release(layers)
+        del layers, gs, fn
+        torch.cuda.empty_cache()
+
+    if not args.quick:
+        # ---- one layer's products at one minute of audio, per-row, one graph a step
+        prods = make_layer(pk, torch, M, seed=1)
+        step = layer_step(pk, prods)
+        graph = graph_of(torch, step)
+        replay_ok = check_replay(pk, torch, prods, graph)
+        lms = time_graph(torch, graph, 50, 5)
+        ops = sum(p.ops() for p in prods)
+        ltops = ops / (lms * 1e-3) / 1e12
+        per750, dom750, dname750, dkms750 = dominant(pk, torch, prods, launches=64, reps=5)
+        extra["layer_M750"] = dict(ms_per_step=round(lms, 5), tops=round(ltops, 1),
+                                   pct_mfma_peak=round(100 * ltops / MFMA_INT8_PEAK_TOPS, 2),
+                                   graph_replay_matches_eager=replay_ok, per_product=per750,
+                                   roofline=roofline_of(dom750, dname750, dkms750),
+                                   layer_quantize_bytes=sum(p.quant_bytes() for p in prods),
+                                   layer_gemm_bytes=sum(p.gemm_bytes() for p in prods))
+        log(f"layer M=750: {lms:.4f} ms a step, {ltops:.1f} TOPS")
+        host_inputs = [(p.x_host.reshape(-1), p.w, p.ws, p.M, p.K, p.N, p.add) for p in prods]
+
+        # the real encoder's blocks (qb = 32 by default, 64 in its fast mode): the
+        # same layer with blocked quantizes and products on the packed path, q, k,
+        # v and pos in one launch as in the per-row step
+        blocked = {}
+        for qb in (32, 64):
+            bd = {p.name: torch.empty((p.M * p.K // qb,), dtype=torch.float32, device=p.x.device) for p in prods}
+            src = {p.name: p for p in prods}
+            owner = {"k": "q", "v": "q"}
+            pos = src["pos"]
+            pk.quantize_packed_dev(None, pos.qp, bd["pos"], pos.x, pos.K, pos.M, pos.xs, qb=qb)  # once an encode
+
+            def blocked_step(qb=qb, bd=bd):
+                for p in prods:
+                    o = src[owner.get(p.name, p.name)]
+                    if p.name not in owner and p.name != "pos":
+                        pk.quantize_packed_dev(None, p.qp, bd[p.name], p.x, p.K, p.M, p.xs, qb=qb)
+                    if p.name in ATTENTION:
+                        if p.name == ATTENTION[0]:
+                            group = [(a, src[owner.get(a.name, a.name)]) for a in prods if a.name in ATTENTION]
+                            pk.gemm_q8_batch_dev([(a.out, a.N, a.m, 0, a.N, a.m.dev_scales, None, ao.qp, bd[ao.name],
+                                                   a.K, a.M, a.add) for a, ao in group], qb=qb)
+                        continue
+                    pk.gemm_q8_packed_dev(p.out, p.N, p.m, 0, p.N, p.m.dev_scales, None, o.qp, bd[o.name], p.K, p.M,
+                                          p.add, qb=qb)
+            gb = graph_of(torch, blocked_step)
+            bms = time_graph(torch, gb, 50, 5)
+            blocked[f"qb{qb}"] = dict(ms_per_step=round(bms, 4), tops=round(ops / (bms * 1e-3) / 1e12, 1),
+                                      kernel=pk.last_kernel())
+            log(f"layer qb={qb}: {bms:.4f} ms")
+            del gb
+        extra["layer_M750_blocked"] = blocked
+
+        # the device-resident layer (the whole of core/encoder.c's layer in HBM:
+        # fused layer norm, SiLU and depthwise producers, the attention's float
+        # products, the eleven products), in the encoder's blocks
+        dlayer = {}
+        host_layer = None
+        for qb in (32, 64):
+            us, host = device_layer(pk, torch, M, qb)
+            dlayer[f"qb{qb}"] = dict(us_per_layer=round(us, 1),
+                                     encoder_ms_per_audio_minute_24_layers=round(us * 24e-3, 2),
+                                     int8_product_tops=round(ops / (us * 1e-6) / 1e12, 1))
+            log(f"device layer qb={qb}: {us:.1f} us")
+            if qb == 32:
+                host_layer = host
+            torch.cuda.empty_cache()
+        extra["device_layer_M750"] = dlayer
+
         # the long-form layer, M = 7500 (one segment of ten minutes)
         long_prods = make_layer(pk, torch, 7500, seed=2)
         gl = graph_of(torch, layer_step(pk, long_prods))
-        lms = time_graph(torch, gl, 10, 3)
+        lfms = time_graph(torch, gl, 10, 3)
         lops = sum(p.ops() for p in long_prods)
-        long_per = {}
-        for p in long_prods:
-            kms = kernel_ms(pk, torch, p, launches=8, reps=2)
-            long_per[p.name] = dict(us=round(kms * 1e3, 1), tops=round(p.ops() / (kms * 1e-3) / 1e12, 1),
-                                    pct_mfma=round(100 * p.ops() / (kms * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS, 1),
-                                    kernel=pk.last_kernel())
-        log(f"long form: {lms:.3f} ms a layer")
-        extra["long_form_M7500"] = dict(ms_per_layer=round(lms, 4), tops=round(lops / (lms * 1e-3) / 1e12, 1),
-                                        pct_mfma_peak=round(100 * lops / (lms * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS, 1),
-                                        per_product=long_per)
+        log(f"long form: {lfms:.3f} ms a layer")
+        extra["long_form_M7500"] = dict(ms_per_layer=round(lfms, 4), tops=round(lops / (lfms * 1e-3) / 1e12, 1),
+                                        pct_mfma_peak=round(100 * lops / (lfms * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS,
+                                                            1))
         for p in long_prods:
             p.m.release()
         del long_prods, gl
@@ -718,24 +926,6 @@ def main():
         for p, _ in rag:
             p.m.release()
         del rag, grg
-
-        # the 24-layer chained sweep, ms of encoder products per audio-minute
-        sweep = {}
-        for Ms in (750, 7500):
-            fn, sops, layers = encoder_sweep(pk, torch, Ms, seed=10 + Ms)
-            gs = graph_of(torch, fn)
-            sms = time_graph(torch, gs, 5 if Ms == 750 else 2, 1)
-            minutes = Ms / 750.0
-            log(f"encoder sweep M={Ms}: {sms:.3f} ms")
-            sweep[f"M{Ms}"] = dict(ms_total=round(sms, 3), ms_per_audio_minute=round(sms / minutes, 4),
-                                   tops=round(sops / (sms * 1e-3) / 1e12, 1),
-                                   weights_MB=round(sum(p.N * p.K for lay in layers for p in lay.values()) / 1e6, 1))
-            for lay in layers:
-                for p in lay.values():
-                    p.m.release()
-            del layers, gs, fn
-            torch.cuda.empty_cache()
-        extra["encoder_24_layers"] = sweep
 
         # skinny shapes against HBM
         extra["skinny"] = skinny_rates(pk, torch, [(1024, 4096, 4096), (4096, 1024, 1024), (640, 1040, 1030)])
@@ -822,49 +1012,50 @@ def main():
             note="host pointers: x or q, d H2D and out D2H over PCIe inside each call, through pinned staging")
         log("host drop-in done")
         if not args.no_cpu:
-            cpu = cpu_baseline(host_inputs, args.cpu_seconds)
-            log("cpu baseline done")
+            lc = cpu_baseline(host_inputs, args.cpu_seconds / 2)
+            extra["layer_M750"]["cpu"] = {k: dict(tops=round(v["tops"], 4), cores=v["cores"], kind=v["kind"],
+                                                  frames_frac=v["frac"], seconds=round(v["seconds"], 1))
+                                          for k, v in lc.items()}
+            log("cpu layer products done")
             w, x, ape = host_layer
-            extra["device_layer_M750"]["cpu_qb32"] = cpu_layer(w, x, ape, M, 32, args.cpu_seconds)
+            extra["device_layer_M750"]["cpu_qb32"] = cpu_layer(w, x, ape, M, 32, args.cpu_seconds / 2)
             log("cpu layer done")
+        for p in prods:
+            p.m.release()
 
     line = {
         "metric": "int8 GEMM TOPS (% of MFMA peak); encoder-GEMM ms per audio-minute, 1 GPU",
-        "value": round(tops, 2),
-        "unit": "TOPS",
+        "value": round(value, 4),
+        "unit": "ms per audio-minute",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded int8 weights, fp32 N(0,1) inputs; random-init weights of the layer's shapes)",
-        "config": {"workload": "FastConformer layer int8 products at M=750 (1 min audio): q,k,v,o,pos(2M-1),"
-                               "ff1/ff2 up 1024->4096 and down 4096->1024, pw1 1024->2048, pw2; "
-                               "per-row quantize + gemm_q8 each, one HIP graph a step",
-                   "M": M, "d_model": 1024, "ff": 4096, "qb": "per-row (n)", "products": len(prods),
-                   "ops_per_step": ops},
+        "data": "synthetic (seeded int8 weights uniform [-127, 127], per-channel scales; fp32 N(0,1) input "
+                "frames; random-init weights of the encoder's shapes, no checkpoint)",
+        "config": {"workload": f"24-layer FastConformer encoder int8 GEMM sweep at M={SWEEP_M} frames (ten "
+                               "minutes of audio, one segment): every layer's q,k,v,o, positions (2M-1 rows), "
+                               "ff1/ff2 up 1024->4096 and down 4096->1024, pw1 1024->2048, pw2 1024->1024, "
+                               "independent weights (~0.6 GB int8 resident), each product's input the previous "
+                               "one's fp32 output quantized per row; one HIP graph a sweep",
+                   "M": SWEEP_M, "layers": 24, "d_model": 1024, "ff": 4096, "qb": "per-row (n)",
+                   "audio_minutes": minutes, "ops_per_step": sops, "tops": round(tops, 1),
+                   "pct_mfma_peak": round(100 * tops / MFMA_INT8_PEAK_TOPS, 2)},
         "roofline": roofline,
         "cpu_baseline": None,
         "extra": extra,
     }
     if cpu:
-        first = next(iter(cpu.values()))
-        name = next(iter(cpu))
-        line["cpu_baseline"] = dict(value=round(first["tops"], 4), unit="TOPS", cores=first["cores"],
-                                    kind=first["kind"],
-                                    sample=f"the same layer's 11 products (quantize + gemm_q8, M=750) on "
-                                           f"{name}, {first['reps']} passes in {first['seconds']:.1f} s, "
-                                           f"{first['cores']} threads, {cpu_model()}")
-        if "ref" in cpu and name != "ref":
-            r = cpu["ref"]
-            line["extra"]["cpu_ref_scalar"] = dict(tops=round(r["tops"], 5), cores=r["cores"], kind=r["kind"],
-                                                   sample=f"ref scalar on {int(r['frac'] * 100)}% of the frames, "
-                                                          f"{r['reps']} passes in {r['seconds']:.1f} s")
-    for p in prods:
-        p.m.release()
+        line["cpu_baseline"] = dict(
+            value=round(cpu["ms_per_audio_minute"], 2), unit="ms per audio-minute", cores=cpu["cores"],
+            kind=cpu["kind"],
+            sample=f"the same sweep (same weights and input, M={cpu['frames']}) on the reference's "
+                   f"{cpu['backend']} kernels dealt over {cpu['cores']} threads: {cpu['layers']} layers of the "
+                   f"chain (passes over its 24) in {cpu['seconds']} s, the time a layer times 24; {cpu_model()}")
     print(json.dumps(line))
 
 
