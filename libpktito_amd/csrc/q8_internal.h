@@ -74,7 +74,13 @@ struct GemmArgs {
     int8_t *oqp = nullptr;
     float *od = nullptr;
     uint32_t oqb = 0;
+    /* 1: plain output stores; 0: non-temporal (set by the launch from the
+     * size of its outputs, kPlainStoreBytes) */
+    int plain = 0;
 };
+
+/* Outputs of a launch above this many bytes are stored plain. */
+constexpr uint64_t kPlainStoreBytes = (uint64_t)64 << 20;
 
 int launch_repack(int8_t *dst, const int8_t *src, uint32_t rows, uint32_t cols, hipStream_t s);
 

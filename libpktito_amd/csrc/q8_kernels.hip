@@ -689,11 +689,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const Seg &sg, uint
                     ov.z = old.z + ov.z;
                     ov.w = old.w + ov.w;
                 }
-                store_out4(o, ov);
+                store_out4(o, ov, g.plain);
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    store_out1(o + r, g.add ? o[r] + v[r] : v[r]);
+                    store_out1(o + r, g.add ? o[r] + v[r] : v[r], g.plain);
             }
         }
     }
@@ -789,7 +789,7 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
         float v = __builtin_fmaf((float)s[r], dt, 0.0f) * wsr[r];
         if (g.bias)
             v = v + br[r];
-        store_out1(o + r, g.add ? old[r] + v : v);
+        store_out1(o + r, g.add ? old[r] + v : v, g.plain);
     }
 }
 
@@ -993,11 +993,11 @@ __device__ __forceinline__ void ring_tile(const GemmArgs &g, const Seg &sg, uint
                     ov.z = old.z + ov.z;
                     ov.w = old.w + ov.w;
                 }
-                store_out4(o, ov);
+                store_out4(o, ov, g.plain);
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    store_out1(o + r, g.add ? o[r] + v[r] : v[r]);
+                    store_out1(o + r, g.add ? o[r] + v[r] : v[r], g.plain);
             }
         }
     }
@@ -1470,11 +1470,11 @@ __device__ __forceinline__ void pipe_tile(const GemmArgs &g, const Seg &sg, uint
                     ov.z = old.z + ov.z;
                     ov.w = old.w + ov.w;
                 }
-                store_out4(o, ov);
+                store_out4(o, ov, g.plain);
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    store_out1(o + r, g.add ? o[r] + v[r] : v[r]);
+                    store_out1(o + r, g.add ? o[r] + v[r] : v[r], g.plain);
             }
         }
     }
@@ -1751,13 +1751,15 @@ static void run_mode(const GemmArgs &g, const SegTable &tab, hipStream_t s, int 
         run_tiled<WN, WM, TN, TM, 2>(g, tab, s);
 }
 
-int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const char **name) {
+int launch_gemm(const GemmArgs &ga, const SegTable &tab, hipStream_t s, const char **name) {
     uint64_t frames = 0;
     uint32_t tmax = 0;
     for (uint32_t i = 0; i < tab.nseg; i++) {
         frames += tab.s[i].T;
         tmax = tab.s[i].T > tmax ? tab.s[i].T : tmax;
     }
+    GemmArgs g = ga;
+    g.plain = frames * ga.rows * 4 > kPlainStoreBytes;
     if (frames == 0 || g.rows == 0)
         return 0;
     const int mode = g.qb == g.n ? 0 : g.qb % 64 == 0 ? 1 : 2;
@@ -1825,13 +1827,17 @@ int launch_gemm(const GemmArgs &g, const SegTable &tab, hipStream_t s, const cha
     return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_gemm_batch(const JobTable &jobs, hipStream_t s, const char **name) {
+int launch_gemm_batch(const JobTable &jobs_in, hipStream_t s, const char **name) {
     uint32_t rows = 0;
-    uint64_t frames = 0;
-    for (uint32_t j = 0; j < jobs.njobs; j++) {
-        rows = jobs.g[j].rows > rows ? jobs.g[j].rows : rows;
-        frames += jobs.s[j].T;
+    uint64_t frames = 0, outs = 0;
+    for (uint32_t j = 0; j < jobs_in.njobs; j++) {
+        rows = jobs_in.g[j].rows > rows ? jobs_in.g[j].rows : rows;
+        frames += jobs_in.s[j].T;
+        outs += (uint64_t)jobs_in.s[j].T * jobs_in.g[j].rows * 4;
     }
+    JobTable jobs = jobs_in;
+    for (uint32_t j = 0; j < jobs.njobs; j++)
+        jobs.g[j].plain = outs > kPlainStoreBytes;
     if (jobs.njobs == 0 || frames == 0)
         return 0;
     /* the tiling the jobs would take as one product of their frames; every

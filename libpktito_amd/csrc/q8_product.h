@@ -14,17 +14,27 @@
 
 namespace pkq8 {
 
-/* Output stores: non-temporal (the products never read their outputs back,
- * and a product's outputs all leave at its end: measured, the stores drain
- * 12-21% sooner this way); the bits are the same. */
+/* Output stores: non-temporal unless the launch sets plain (GemmArgs::plain,
+ * uniform). Measured: a product of up to a few tens of MB of outputs drains
+ * its stores 12-21% sooner non-temporal; one of ~120 MB (the feed-forward
+ * up projection at ten minutes of audio) runs ~7% sooner with plain stores.
+ * The bits are the same. */
 typedef float nt_f4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void store_out4(float *o, float4 v) {
+__device__ __forceinline__ void store_out4(float *o, float4 v, int plain) {
     const nt_f4 nv = { v.x, v.y, v.z, v.w };
-    __builtin_nontemporal_store(nv, (nt_f4 *)o);
+    if (plain)
+        *(nt_f4 *)o = nv;
+    else
+        __builtin_nontemporal_store(nv, (nt_f4 *)o);
 }
 
-__device__ __forceinline__ void store_out1(float *o, float v) { __builtin_nontemporal_store(v, o); }
+__device__ __forceinline__ void store_out1(float *o, float v, int plain) {
+    if (plain)
+        *o = v;
+    else
+        __builtin_nontemporal_store(v, o);
+}
 
 #define PK_AS1(p) ((const void __attribute__((address_space(1))) *)(p))
 #define PK_AS3(p) ((void __attribute__((address_space(3))) *)(p))
