@@ -319,7 +319,10 @@ def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20, rows=(1, 4, 16), lau
     """Skinny products: M in {1, 4, 16} rows through weights rotated over more than
     512 MB of distinct matrices, so that L2 and the 256 MB MALL serve none of
     them. One graph of launches over the copies; GB/s from the algorithmic
-    bytes N K + 4 N + M K + 4 M + 4 M N of each launch."""
+    bytes N K + 4 N + M K + 4 M + 4 M N of each launch. Beside each, the
+    floors it is read against, in graphs of as many launches: an empty
+    kernel, and a streaming read of the same bytes through a rotation of the
+    same size (of_stream_read: the read's time over the product's)."""
     from libpktito_amd import synth
     dev = torch.device("cuda")
     out = []
@@ -333,6 +336,9 @@ def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20, rows=(1, 4, 16), lau
         for c in range(copies):
             wslice = big[c * per:(c + 1) * per]
             mats.append(pk.Q8Matrix(wslice, wsa))
+        rot = torch.empty((copies * per + 64 * 1024,), dtype=torch.uint8, device=dev)
+        rot.random_(0, 256)
+        sink = torch.zeros((4,), dtype=torch.int32, device=dev)
         for M in rows:
             x = torch.from_numpy(synth.activations(g, M, K)).to(dev)
             q = torch.empty((M, K), dtype=torch.int8, device=dev)
@@ -355,14 +361,29 @@ def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20, rows=(1, 4, 16), lau
                     pk.gemm_q8_dev(o, N, m, 0, N, None, None, q, d, K, K, M, 0, ws_ptr=m.dev_scales)
             gr = graph_of(torch, fn)
             ms = min(time_graph(torch, gr, 2, 1) for _ in range(3)) / len(mats)
+            kname = pk.last_kernel()
             byts = N * K + 4 * N + M * K + 4 * M + 4 * M * N
+            # the yardsticks: the same number of back-to-back launches of an
+            # empty kernel, and of a streaming read of the same bytes through
+            # a rotation of the same size
+            rd = (byts + 15) // 16 * 16
+
+            def read():
+                for c in range(len(mats)):
+                    pk.stream_read_dev(rot[c * per:], sink, nbytes=rd)
+            gs = graph_of(torch, read)
+            rms = min(time_graph(torch, gs, 2, 1) for _ in range(3)) / len(mats)
+            ge = graph_of(torch, lambda: [pk.empty_dev() for _ in mats])
+            ems = min(time_graph(torch, ge, 2, 1) for _ in range(3)) / len(mats)
+            del gr, gs, ge
             out.append(dict(M=M, K=K, N=N, outputs=real, us=round(ms * 1e3, 3),
                             GBs=round(byts / (ms * 1e-3) / 1e9, 1),
                             hbm_frac=round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3),
-                            kernel=pk.last_kernel()))
+                            stream_read_us=round(rms * 1e3, 3), empty_launch_us=round(ems * 1e3, 3),
+                            of_stream_read=round(rms / ms, 3), kernel=kname))
         for m in mats:
             m.release()
-        del big
+        del big, rot
     return out
 
 

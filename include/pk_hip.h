@@ -316,6 +316,16 @@ int pk_hip_lstm_step_dev(float *h_out, float *c, const float *h_in, const float 
 int pk_hip_joint_dev(float *logit, uint32_t *tok_dur, const pk_hip_q8 *jout, const float *jout_b, const float *f,
                      const float *gp, uint32_t V, uint32_t n_dur, void *stream);
 
+/* Measurement aids, with no counterpart in the reference: the floors a
+ * small product's time is read against. pk_hip_empty_dev launches an empty
+ * kernel; pk_hip_stream_read_dev reads the bytes at p (16-byte aligned,
+ * bytes a multiple of 16) with one 16-byte load a thread over as many
+ * workgroups as they need, and writes *sink only if the loads' fold meets a
+ * fixed constant (so nothing is written in practice; sink is device
+ * memory). */
+int pk_hip_empty_dev(void *stream);
+int pk_hip_stream_read_dev(const void *p, size_t bytes, uint32_t *sink, void *stream);
+
 /* The kernel variant the calling thread launched last, for profiling and
  * tests. */
 const char *pk_hip_last_kernel(void);

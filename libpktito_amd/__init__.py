@@ -123,6 +123,8 @@ _SIGS = {
     "pk_hip_attention_workspace": (ctypes.c_size_t, [ctypes.c_uint32, ctypes.c_uint32]),
     "pk_hip_attention_dev": (ctypes.c_int, [ctypes.c_void_p] * 7 + [ctypes.c_uint32] * 3 +
                              [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "pk_hip_empty_dev": (ctypes.c_int, [ctypes.c_void_p]),
+    "pk_hip_stream_read_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]),
     "pk_hip_attention_noalloc_dev": (ctypes.c_int, [ctypes.c_void_p] * 7 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]),
     "pk_hip_layer_workspace": (ctypes.c_size_t, [ctypes.POINTER(LayerW), ctypes.c_uint32, ctypes.c_uint32]),
     "pk_hip_gemv_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -391,6 +393,19 @@ def attention_noalloc_dev(o, q, k, v, p, bias_u, bias_v, T, D, H, stream=None):
     workspace, nothing allocated (pk_hip_attention_noalloc_dev)."""
     _check(lib().pk_hip_attention_noalloc_dev(_dptr(o), _dptr(q), _dptr(k), _dptr(v), _dptr(p), _dptr(bias_u),
                                               _dptr(bias_v), T, D, H, _stream(stream)))
+
+
+def empty_dev(stream=None):
+    """An empty kernel launch (the launch floor, for measurements)."""
+    _check(lib().pk_hip_empty_dev(_stream(stream)))
+
+
+def stream_read_dev(buf, sink, nbytes=None, stream=None):
+    """A streaming read of nbytes (all of buf by default) of the device tensor
+    buf, sink a device tensor of at least 4 bytes (the read floor, for
+    measurements)."""
+    n = buf.numel() * buf.element_size() if nbytes is None else nbytes
+    _check(lib().pk_hip_stream_read_dev(_dptr(buf), n, _dptr(sink), _stream(stream)))
 
 
 class DeviceLayer:

@@ -1197,4 +1197,26 @@ int pk_hip_joint_dev(float *logit, uint32_t *tok_dur, const pk_hip_q8 *jout, con
     return PK_HIP_OK;
 }
 
+int pk_hip_empty_dev(void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    PK_LAUNCH(pkq8::launch_empty((hipStream_t)stream), "empty launch");
+    g_kernel = "empty";
+    return PK_HIP_OK;
+}
+
+int pk_hip_stream_read_dev(const void *p, size_t bytes, uint32_t *sink, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (bytes == 0)
+        return PK_HIP_OK;
+    if (!p || !sink || bytes % 16 || (uintptr_t)p % 16)
+        return fail(PK_HIP_EINVAL, "stream_read_dev: p and sink set, p 16-byte aligned, bytes a multiple of 16");
+    PK_LAUNCH(pkq8::launch_stream_read(p, bytes, sink, (hipStream_t)stream), "stream read launch");
+    g_kernel = "stream_read";
+    return PK_HIP_OK;
+}
+
 }  // extern "C"

@@ -147,6 +147,11 @@ int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstr
                  const float *bias, const float *f, const float *gp, uint32_t rows, uint32_t J, uint32_t kr,
                  uint32_t V, uint32_t n_dur, hipStream_t s);
 
+/* Measurement aids (diag_kernels.hip): an empty launch; a streaming read of
+ * bytes (a multiple of 16) at p, 16-byte aligned. */
+int launch_empty(hipStream_t s);
+int launch_stream_read(const void *p, uint64_t bytes, uint32_t *sink, hipStream_t s);
+
 /* One product; table->nseg == 1 for a plain call. With g.oqp set, -3 where
  * the fused SiLU quantize is not available (nothing launched). */
 int launch_gemm(const GemmArgs &g, const SegTable &table, hipStream_t s, const char **name);
