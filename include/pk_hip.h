@@ -99,8 +99,10 @@ void pk_hip_release_all(void);
 /* -------------------------------------------------------- the drop-in --- */
 
 /* The table's quantize (backend/kernels.h:47-58, :256), on host pointers:
- * a->q, a->d and x are host memory; returns with q and d written.
- * Round-to-nearest only (PK_HIP_EROUND otherwise). */
+ * a->q, a->d and x are host memory; returns with q and d written. Follows
+ * the calling thread's rounding mode as the reference's ref does (both
+ * divisions, the product and rintf; backend/ref/kernels.c:24-58); the
+ * device-pointer quantizes below round to nearest. */
 int pk_hip_quantize(pk_hip_act *a, const float *x, size_t xs);
 
 /* The table's gemm_q8 (backend/kernels.h:60-78, :257-258), on host pointers:

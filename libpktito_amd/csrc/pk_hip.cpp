@@ -339,9 +339,10 @@ int check_act(const pk_hip_act *a, bool for_gemm) {
     return PK_HIP_OK;
 }
 
-int launch_quant(pk_hip_act *a, const float *x, size_t xs, hipStream_t s) {
+int launch_quant(pk_hip_act *a, const float *x, size_t xs, hipStream_t s, int rmode = 0) {
     const char *name = "";
-    if (const int r = pkq8::launch_quantize(a->q, a->d, x, xs, a->n, a->qb, a->T, s, &name))
+    if (const int r = rmode ? pkq8::launch_quantize_directed(a->q, a->d, x, xs, a->n, a->qb, a->T, rmode, s, &name)
+                            : pkq8::launch_quantize(a->q, a->d, x, xs, a->n, a->qb, a->T, s, &name))
         return launch_fail(r, "quantize launch");
     g_kernel = name;
     return PK_HIP_OK;
@@ -548,8 +549,11 @@ int pk_hip_quantize(pk_hip_act *a, const float *x, size_t xs) {
         return PK_HIP_OK;
     if (!x || xs < a->n)
         return fail(PK_HIP_EINVAL, "quantize: x is NULL or its stride %zu is under n %u", xs, a->n);
-    if (rmode_of_host() != 0)
-        return fail(PK_HIP_EROUND, "quantize runs to nearest only");
+    /* the calling thread's rounding mode, which the reference's ref follows
+     * in both divisions, the product and rintf */
+    const int rmode = rmode_of_host();
+    if (rmode < 0)
+        return fail(PK_HIP_EROUND, "quantize: unknown rounding mode");
     Lease l;
     if ((e = lease(l)))
         return e;
@@ -564,7 +568,7 @@ int pk_hip_quantize(pk_hip_act *a, const float *x, size_t xs) {
     if ((e = h2d(l.c, dx, x, n * sizeof(float), T, xs * sizeof(float))))
         return e;
     pk_hip_act da = { dq, dd, a->n, a->qb, a->T };
-    if ((e = launch_quant(&da, dx, n, s)))
+    if ((e = launch_quant(&da, dx, n, s, rmode)))
         return e;
     if ((e = d2h(l.c, a->q, n, dq, n, T)) || (e = d2h(l.c, a->d, nb * sizeof(float), dd, nb * sizeof(float), T)))
         return e;

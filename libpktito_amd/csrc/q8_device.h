@@ -31,6 +31,51 @@ __device__ __forceinline__ int pack4(float4 v, float id) {
            (q1(v.w, id) & 0xff) << 24;
 }
 
+/* The quantizer under a directed rounding mode rm (1 upward, 2 downward, 3
+ * toward zero), as the reference's ref computes it when the host has set one
+ * (its divisions, product and rintf all follow the mode). A division is
+ * taken from its round-to-nearest quotient r and the sign of its remainder
+ * a - r b, exact as one fmaf (also where r is subnormal: amax >= 2^-121 is a
+ * multiple of 2^-144 and r b one of 2^-149), so the directed quotient is r
+ * or its neighbour toward the true value; the product and rintf run with
+ * the hardware's rounding mode set (ref_rintf). */
+__device__ __forceinline__ float next_up(float x) {
+    /* x finite; the neighbour toward +inf (the smallest subnormal after a zero) */
+    const int b = __float_as_int(x);
+    if ((b & 0x7fffffff) == 0)
+        return __int_as_float(1);
+    return __int_as_float(x > 0.0f ? b + 1 : b - 1);
+}
+
+__device__ __forceinline__ float next_down(float x) { return -next_up(-x); }
+
+__device__ __forceinline__ float round_dir(float r, bool above, bool below, int rm) {
+    if (rm == 1)
+        return above ? next_up(r) : r;
+    if (rm == 2)
+        return below ? next_down(r) : r;
+    return r > 0.0f && below ? next_down(r) : r < 0.0f && above ? next_up(r) : r;
+}
+
+/* a / b, b > 0 */
+__device__ __forceinline__ float div_dir(float a, float b, int rm) {
+    const float r = a / b;
+    const float rem = __builtin_fmaf(-r, b, a);
+    return round_dir(r, rem > 0.0f, rem < 0.0f, rm);
+}
+
+/* rintf as the reference's ref computes it on x86: built at -O3 without
+ * SSE4.1, gcc inlines rintf(x) as copysign((|x| + 2^23) - 2^23, x) for |x| <
+ * 2^23 (x itself otherwise), both operations in the current mode. To nearest
+ * that is rint; under a directed mode it rounds |x|, so upward -43.18 gives
+ * -44. The caller has set MODE.FP_ROUND to the mode. */
+__device__ __forceinline__ float ref_rintf(float x) {
+    const float a = __builtin_fabsf(x);
+    if (!(a < 8388608.0f))
+        return x;
+    return __builtin_copysignf((a + 8388608.0f) - 8388608.0f, x);
+}
+
 /* The same block rule on magnitude bits: m = the largest (bits & 0x7fffffff)
  * of the block. Non-negative floats order as their bit patterns do, NaN above
  * infinity above every finite value, so the block holds a NaN or an infinity

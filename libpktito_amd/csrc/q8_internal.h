@@ -87,6 +87,11 @@ int launch_repack(int8_t *dst, const int8_t *src, uint32_t rows, uint32_t cols, 
 int launch_quantize(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb,
                     uint32_t T, hipStream_t s, const char **name);
 
+/* The quantizer under a directed rounding mode (rm 1 upward, 2 downward, 3
+ * toward zero), one thread a block: -2 for rm or qb it does not take. */
+int launch_quantize_directed(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb, uint32_t T,
+                             int rm, hipStream_t s, const char **name);
+
 /* Quantize (n <= 4096; qb == n, 32 or 64) writing the packed copy qp, and
  * the row-major q too when q is not NULL. */
 int launch_quantize_packed(int8_t *q, int8_t *qp, float *d, const float *x, size_t xs, uint32_t n,

@@ -182,6 +182,55 @@ __global__ __launch_bounds__(256) void quant_any_kernel(int8_t *__restrict__ q, 
     d[i] = dv;
 }
 
+/* The quantizer under a directed rounding mode (rm 1 upward, 2 downward, 3
+ * toward zero): one thread a block, the reference's loop; the divisions
+ * from their nearest quotients (div_dir), the product and ref's rintf in
+ * the hardware's mode. The host entry launches it when the calling
+ * thread's mode is not to nearest. */
+__global__ __launch_bounds__(256) void quant_directed_kernel(int8_t *__restrict__ q, float *__restrict__ d,
+                                                             const float *__restrict__ x, size_t xs, uint32_t n,
+                                                             uint32_t qb, uint32_t T, int rm) {
+    const uint32_t nb = n / qb;
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (uint64_t)T * nb)
+        return;
+    const uint32_t t = (uint32_t)(i / nb), b = (uint32_t)(i % nb);
+    const float *v = x + (size_t)t * xs + (size_t)b * qb;
+    int8_t *qq = q + (size_t)t * n + (size_t)b * qb;
+    float amax = 0.0f;
+    int nan = 0;
+    for (uint32_t k = 0; k < qb; k++) {
+        nan |= v[k] != v[k];
+        amax = fmaxf(amax, fabsf(v[k]));
+    }
+    if (zero_block(amax, nan)) {
+        for (uint32_t k = 0; k < qb; k++)
+            qq[k] = 0;
+        d[i] = 0.0f;
+        return;
+    }
+    /* the divisions to nearest and corrected; then the mode for the rest */
+    float id = div_dir(127.0f, amax, rm), dv = div_dir(amax, 127.0f, rm);
+    asm volatile("" : "+v"(id), "+v"(dv));
+    __builtin_amdgcn_s_setreg(2049, __builtin_amdgcn_readfirstlane(rm));    /* MODE.FP_ROUND, single */
+    asm volatile("" : "+v"(id));
+    for (uint32_t k = 0; k < qb; k++)
+        qq[k] = (int8_t)((int)ref_rintf(v[k] * id) & 0xff);
+    d[i] = dv;
+}
+
+int launch_quantize_directed(int8_t *q, float *d, const float *x, size_t xs, uint32_t n, uint32_t qb, uint32_t T,
+                             int rm, hipStream_t s, const char **name) {
+    if (T == 0)
+        return 0;
+    if (rm < 1 || rm > 3 || qb == 0 || n % qb)
+        return -2;
+    const uint64_t blocks = (uint64_t)T * (n / qb);
+    quant_directed_kernel<<<(uint32_t)((blocks + 255) / 256), 256, 0, s>>>(q, d, x, xs, n, qb, T, rm);
+    *name = "quant_directed";
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
+}
+
 /* One wave a column of n <= 4096 inputs, four columns a workgroup (the
  * quantizes of up to about 7M inputs, where the kernel is one memory round
  * trip and wants its loads spread over the most CUs). */

@@ -70,6 +70,40 @@ def quant_tiny():
     return x, T, n, qb, top
 
 
+def quant_directed_cases(seed=300):
+    """Inputs for the quantizer under directed rounding (ref follows the host's
+    mode in amax / 127, 127 / amax, v * id and rintf): (x, T, n, qb, xs).
+    Rows 0-6 of each carry the edges: blocks at and just above the 2^-121
+    zero rule (subnormal d), a constant block (products of 127 exactly),
+    small integers, a large value beside tiny, subnormal and signed-zero
+    ones (products under 1/2), halves (products on .5), a NaN and an
+    infinity; the rest N(0, 9), whose largest value reaches rint 128 upward."""
+    out = []
+    for i, (T, n, qb, pad) in enumerate([(37, 256, 32, 0), (37, 256, 64, 32), (21, 256, 256, 0), (9, 1024, 1024, 32),
+                                         (5, 64, 32, 0)]):
+        g = synth.rng(seed + i)
+        xs = n + pad
+        x = (g.standard_normal(T * xs) * 3).astype(np.float32)
+        r = [x[t * xs:t * xs + n] for t in range(min(T, 7))]
+        r[0][:] = np.float32(2.0 ** -121) * g.standard_normal(n).astype(np.float32)
+        r[1][:] = np.float32(2.0 ** -119)
+        r[2][:] = (np.arange(n) % 33 - 16).astype(np.float32)
+        r[3][:] = g.uniform(-1e-3, 1e-3, n).astype(np.float32)
+        r[3][::8] = np.float32(100.0)
+        r[3][1::8] = np.float32(1e-40)
+        r[3][2::8] = np.float32(-0.0)
+        r[3][3::8] = np.float32(-1e-40)
+        if len(r) > 4:
+            r[4][:] = (np.arange(n) % 16 - 8).astype(np.float32) + np.float32(0.5)
+            r[4][::qb] = np.float32(127.0)
+        if len(r) > 5:
+            r[5][qb // 2] = np.nan
+        if len(r) > 6:
+            r[6][(qb + 1) % n] = np.inf
+        out.append((x, T, n, qb, xs))
+    return out
+
+
 def quant_random_params(count, seed=100):
     """kcheck's run(): n = 32 * (1 + r % 40), T in [1, 20], qb 32 or n,
     xs = n or n + 32, scale 1 or 1e4; and its fast mode's qb = 64."""

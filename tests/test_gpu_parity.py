@@ -157,14 +157,27 @@ def test_rounding_modes(hip, rmode):
             finally:
                 libm.fesetround(0)
         assert same(out, want), (rmode, n, qb, T, f)
-    # quantize refuses a directed rounding rather than computing other bits
-    libm.fesetround(FE[rmode])
-    try:
-        with pytest.raises(hip.PkHipError) as e:
-            hip_quantize(hip, np.ones(64, np.float32), 1, 64, 64, 64)
-    finally:
-        libm.fesetround(0)
-    assert e.value.code == hip.PK_HIP_EROUND
+
+
+@pytest.mark.parametrize("rmode", [1, 2, 3])
+def test_quantize_rounding_modes(hip, rmode):
+    """The table's quantize under the calling thread's directed rounding, as
+    ref follows it (backend/ref/kernels.c:24-58: amax / 127, 127 / amax,
+    v * id and rintf all in the mode): the oracle's bits, itself pinned to
+    ref's under each mode, on the edge inputs of cases.quant_directed_cases
+    (subnormal scales, products under 1/2 and on .5, rint 128 upward wrapped
+    to -128, NaN and infinite blocks, xs > n)."""
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    for (x, T, n, qb, xs) in cases.quant_directed_cases():
+        say("quantize rounding", rmode, T, n, qb, xs)
+        assert libm.fesetround(FE[rmode]) == 0
+        try:
+            wq, wd = ol.quantize(x, T, n, qb, xs)
+            q, d = hip_quantize(hip, x, T, n, qb, xs)
+        finally:
+            libm.fesetround(0)
+        assert hip.last_kernel() == "quant_directed"
+        assert np.array_equal(q, wq) and same(d, wd), (rmode, T, n, qb, xs)
 
 
 def test_upload_rejects_overlapping_bytes(hip):

@@ -109,6 +109,30 @@ def test_oracle_follows_rounding_mode_like_ref(mode):
         assert np.array_equal(bits(o1), bits(o2)), (mode, n, qb, T, f)
 
 
+@needs_ref
+@pytest.mark.parametrize("mode", ["upward", "downward", "towardzero"])
+def test_oracle_quantize_follows_rounding_mode_like_ref(mode):
+    """The quantizer under each directed mode: ref follows the host's mode in
+    both divisions, the product and rintf (backend/ref/kernels.c:24-58), and
+    so does the oracle's restatement, bit for bit on the edge inputs (and
+    unlike the nearest mode on many of them)."""
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    moved = 0
+    for (x, T, n, qb, xs) in cases.quant_directed_cases():
+        qn, dn = ol.quantize(x, T, n, qb, xs)
+        assert libm.fesetround(FE[mode]) == 0
+        try:
+            q1, d1 = ol.quantize(x, T, n, qb, xs)
+            q2, d2 = ol.quantize(x, T, n, qb, xs, impl="ref")
+        finally:
+            libm.fesetround(0)
+        assert np.array_equal(q1, q2) and np.array_equal(bits(d1), bits(d2)), (mode, T, n, qb, xs)
+        moved += int((q1 != qn).sum() + (bits(d1) != bits(dn)).sum())
+        if mode == "upward":
+            assert (q1 == -128).any()           # rint 128 upward, wrapped as ref's conversion wraps it
+    assert moved > 100
+
+
 # ------------------------------------------------------- the mathematics ---
 
 def test_fmaf_is_one_rounding():
