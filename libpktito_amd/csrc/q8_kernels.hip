@@ -1684,8 +1684,6 @@ static const RingCfg kRing[] = {
     { "pipe<64x64,2,4,k2>", 64, 64, 2, 4, 2, run_pipe<2, 2, 2, 2, 2, 4, 2>, run_pipe_batch<2, 2, 2, 2, 2, 4, 2>, nullptr, nullptr },
     { "pipe<64x64,1,4,k2>", 64, 64, 1, 4, 2, run_pipe<2, 2, 2, 2, 1, 4, 2>, run_pipe_batch<2, 2, 2, 2, 1, 4, 2>, nullptr, nullptr },
     { "pipe<64x64,2,2,k2>", 64, 64, 2, 2, 2, run_pipe<2, 2, 2, 2, 2, 2, 2>, run_pipe_batch<2, 2, 2, 2, 2, 2, 2>, nullptr, nullptr },
-    /* four K groups of four waves of 32 x 32 (1024 threads) */
-    { "pipe<64x64,1,4,k4>", 64, 64, 1, 4, 4, run_pipe<2, 2, 2, 2, 1, 4, 4>, run_pipe_batch<2, 2, 2, 2, 1, 4, 4>, nullptr, nullptr },
     /* three slots: three workgroups a CU */
     { "pipe<64x64,2,3>", 64, 64, 2, 3, 1, run_pipe<2, 2, 2, 2, 2, 3, 1>, run_pipe_batch<2, 2, 2, 2, 2, 3, 1>, run_pipe<2, 2, 2, 2, 2, 3, 1, 1>, run_pipe<2, 2, 2, 2, 2, 3, 1, 2>, run_pipe_batch<2, 2, 2, 2, 2, 3, 1, 1>, run_pipe_batch<2, 2, 2, 2, 2, 3, 1, 2> },
     { "pipe<64x64,2,3,k2>", 64, 64, 2, 3, 2, run_pipe<2, 2, 2, 2, 2, 3, 2>, run_pipe_batch<2, 2, 2, 2, 2, 3, 2>, nullptr, nullptr },
