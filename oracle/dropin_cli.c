@@ -11,14 +11,91 @@
  * int8 matrix of the model is uploaded after the load and released before
  * the free: the steps INTEGRATION.md adds to core/model.c (:783-811,
  * :868-883). FAST 1 is the encoder's fast mode, blocks of 64 inputs
- * (pk_asr_set_fast_mode; blocks of 32 otherwise). */
+ * (pk_asr_set_fast_mode; blocks of 32 otherwise).
+ *
+ *   dropin_cli MODEL.pkf SECONDS SEED FAST THREADS --layers OUT
+ *
+ * also writes the reference's own encoder layers (core/encoder.c:338-368,
+ * static, so reached through pk_encode, core/encoder.c:429-506, with the
+ * model's n_layers set to 0, 1, ... in turn on the same features) to OUT:
+ * each layer's input and output, the positions' quantized encodings and
+ * every layer's weights, for the oracle's layer to be compared with. Layout
+ * (little-endian): "PKLD", u32 Te, D, H, F, K, qb, L; f32 eps; f32 x[L + 1]
+ * [Te][D]; i8 ape_q[2Te - 1][D]; f32 ape_d[2Te - 1][D / qb]; then a layer:
+ * f32 ff1_nw, ff1_nb, att_nw, att_nb, conv_nw, conv_nb, ff2_nw, ff2_nb,
+ * out_nw, out_nb, bias_u, bias_v [D]; f32 dw [D][K]; f32 dw_b [D]; and
+ * ff1_up, ff1_down, ff2_up, ff2_down, q, k, v, pos, o, pw1, pw2 each as u32
+ * rows, cols, i8 panels [rows * cols], f32 scales [rows]. */
 #include "pktito.h"
 #include "model.h"
+#include "asr.h"
+#include "mel.h"
 
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+
+static void put(FILE *f, const void *p, size_t bytes) {
+    if (bytes && fwrite(p, 1, bytes, f) != bytes) {
+        fprintf(stderr, "write failed\n");
+        exit(1);
+    }
+}
+
+static void put_u32(FILE *f, uint32_t v) { put(f, &v, 4); }
+
+static void put_q8(FILE *f, const pk_q8 *w) {
+    put_u32(f, w->rows);
+    put_u32(f, w->cols);
+    put(f, w->q, (size_t)w->rows * w->cols);
+    put(f, w->s, (size_t)w->rows * sizeof(float));
+}
+
+/* The encoder's layers one at a time (see the header): pk_asr_run has
+ * sized every buffer for these samples; the features are made once. */
+static int dump_layers(pk_model *m, pk_asr *a, const float *x, size_t n, const char *path) {
+    const uint32_t L = m->n_layers, D = m->d_model;
+    const size_t T0 = pk_mel_frames(m, n);
+    pk_mel(a, x, n);
+    FILE *f = fopen(path, "wb");
+    if (!f)
+        return -1;
+    uint32_t Te = 0;
+    for (uint32_t l = 0; l <= L; l++) {
+        m->n_layers = l;
+        Te = pk_encode(a, (uint32_t)T0);
+        if (!Te || Te >= 100) {     /* a longer input races its layers' threads (core/encoder.c:403-427) */
+            fclose(f);
+            return -1;
+        }
+        if (l == 0) {
+            put(f, "PKLD", 4);
+            const uint32_t hdr[7] = { Te, D, m->n_heads, m->ff_dim, m->conv_kernel, a->ape.qb, L };
+            put(f, hdr, sizeof hdr);
+            put(f, &m->ln_eps, 4);
+        }
+        put(f, a->x, (size_t)Te * D * sizeof(float));
+    }
+    m->n_layers = L;
+    const size_t R = 2 * (size_t)Te - 1;
+    put(f, a->ape.q, R * D);
+    put(f, a->ape.d, R * (D / a->ape.qb) * sizeof(float));
+    for (uint32_t l = 0; l < L; l++) {
+        const pk_layer *y = &m->layers[l];
+        const float *vec[] = { y->ff1_nw, y->ff1_nb, y->att_nw, y->att_nb, y->conv_nw, y->conv_nb,
+                               y->ff2_nw, y->ff2_nb, y->out_nw, y->out_nb, y->bias_u, y->bias_v };
+        for (size_t i = 0; i < sizeof vec / sizeof vec[0]; i++)
+            put(f, vec[i], (size_t)D * sizeof(float));
+        put(f, y->dw, (size_t)D * m->conv_kernel * sizeof(float));
+        put(f, y->dw_b, (size_t)D * sizeof(float));
+        const pk_q8 *mats[] = { &y->ff1_up, &y->ff1_down, &y->ff2_up, &y->ff2_down, &y->q, &y->k, &y->v,
+                                &y->pos, &y->o, &y->pw1, &y->pw2 };
+        for (size_t i = 0; i < sizeof mats / sizeof mats[0]; i++)
+            put_q8(f, mats[i]);
+    }
+    return fclose(f) ? -1 : 0;
+}
 
 int pk_hip_upload_model(const pk_model *m, char *err, size_t errlen);
 void pk_hip_release_model(const pk_model *m);
@@ -78,6 +155,10 @@ int main(int argc, char **argv) {
     printf("tokens %ld\n", c);
     for (long i = 0; i < c; i++)
         printf("%d %d %d\n", toks[i].id, toks[i].frame, toks[i].dur);
+    if (argc >= 8 && !strcmp(argv[6], "--layers") && dump_layers(m, a, x, n, argv[7])) {
+        fprintf(stderr, "layer dump failed\n");
+        return 1;
+    }
     fprintf(stderr, "backend: %s\n", pk_backend());
     pk_asr_free(a);
     if (hip)
