@@ -25,7 +25,18 @@
  * f32 ff1_nw, ff1_nb, att_nw, att_nb, conv_nw, conv_nb, ff2_nw, ff2_nb,
  * out_nw, out_nb, bias_u, bias_v [D]; f32 dw [D][K]; f32 dw_b [D]; and
  * ff1_up, ff1_down, ff2_up, ff2_down, q, k, v, pos, o, pw1, pw2 each as u32
- * rows, cols, i8 panels [rows * cols], f32 scales [rows]. */
+ * rows, cols, i8 panels [rows * cols], f32 scales [rows].
+ *
+ *   dropin_cli MODEL.pkf SECONDS SEED FAST THREADS --decoder OUT
+ *
+ * writes the reference's decoder's input and output instead: the joint's
+ * encoder half of every frame (pk_joint_frames, core/decoder.c:149-156),
+ * the prediction network and joint, and the tokens its search emitted
+ * (core/decoder.c:121-147). Layout: "PKDC", u32 Te, P, L, J, V, n_dur,
+ * blank, max_symbols, dur[n_dur]; f32 f[Te][J]; f32 embed[V + 1][P]; per
+ * LSTM layer wx, wh (u32 rows, cols, i8 panels, f32 scales) and f32 b[4P];
+ * jpred, f32 jpred_b[J]; jout, f32 jout_b[its rows]; u32 ntoks; i32 (id,
+ * frame, dur) a token. */
 #include "pktito.h"
 #include "model.h"
 #include "asr.h"
@@ -97,6 +108,36 @@ static int dump_layers(pk_model *m, pk_asr *a, const float *x, size_t n, const c
     return fclose(f) ? -1 : 0;
 }
 
+/* The decoder's input, weights and tokens after pk_asr_run (see the
+ * header): the run's one chunk left its joint frames in a->fproj[0]. */
+static int dump_decoder(const pk_model *m, const pk_asr *a, uint32_t Te, const char *path) {
+    FILE *f = fopen(path, "wb");
+    if (!f)
+        return -1;
+    const uint32_t P = m->pred_hidden, J = m->joint_hidden;
+    put(f, "PKDC", 4);
+    const uint32_t hdr[8] = { Te, P, m->pred_layers, J, m->vocab, m->n_dur, m->blank, m->max_symbols };
+    put(f, hdr, sizeof hdr);
+    put(f, m->dur, (size_t)m->n_dur * 4);
+    put(f, a->fproj[0], (size_t)Te * J * sizeof(float));
+    put(f, m->embed, (size_t)(m->vocab + 1) * P * sizeof(float));
+    for (uint32_t l = 0; l < m->pred_layers; l++) {
+        put_q8(f, &m->lstm[l].wx);
+        put_q8(f, &m->lstm[l].wh);
+        put(f, m->lstm[l].b, (size_t)4 * P * sizeof(float));
+    }
+    put_q8(f, &m->jpred);
+    put(f, m->jpred_b, (size_t)J * sizeof(float));
+    put_q8(f, &m->jout);
+    put(f, m->jout_b, (size_t)m->jout.rows * sizeof(float));
+    put_u32(f, (uint32_t)a->ntoks);
+    for (size_t i = 0; i < a->ntoks; i++) {
+        const int32_t t3[3] = { a->toks[i].id, a->toks[i].frame, a->toks[i].dur };
+        put(f, t3, sizeof t3);
+    }
+    return fclose(f) ? -1 : 0;
+}
+
 int pk_hip_upload_model(const pk_model *m, char *err, size_t errlen);
 void pk_hip_release_model(const pk_model *m);
 
@@ -155,6 +196,11 @@ int main(int argc, char **argv) {
     printf("tokens %ld\n", c);
     for (long i = 0; i < c; i++)
         printf("%d %d %d\n", toks[i].id, toks[i].frame, toks[i].dur);
+    if (argc >= 8 && !strcmp(argv[6], "--decoder") &&
+        dump_decoder(m, a, (uint32_t)pk_enc_frames((uint32_t)pk_mel_frames(m, n)), argv[7])) {
+        fprintf(stderr, "decoder dump failed\n");
+        return 1;
+    }
     if (argc >= 8 && !strcmp(argv[6], "--layers") && dump_layers(m, a, x, n, argv[7])) {
         fprintf(stderr, "layer dump failed\n");
         return 1;

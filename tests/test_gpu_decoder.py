@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as ol
+from tdt_search import search
 from libpktito_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -179,33 +180,6 @@ def test_argmax_rule(hip, torch):
             assert tuple(dd.tok_dur.cpu().numpy().tolist()) == (tok, dur), k
         finally:
             dd.release()
-
-
-def search(T, predict, joint, blank, durs, max_symbols):
-    """core/decoder.c:104-140, TDT's greedy search, over predict(label) and
-    joint(t) -> (token, duration index)."""
-    toks = []
-    predict(blank)
-    t, last, lasts = 0, None, 0
-    while t < T:
-        while True:
-            at = t
-            k, di = joint(t)
-            d = durs[di]
-            if k == blank and d == 0:
-                d = 1
-            t += d
-            if not (k == blank and t < T):
-                break
-        if k == blank:
-            break
-        toks.append((k, at, durs[di]))
-        lasts = lasts + 1 if last == at else 1
-        last = at
-        predict(k)
-        if lasts >= max_symbols and last == t:
-            t += 1
-    return toks
 
 
 def test_greedy_search_on_device(hip, torch):
