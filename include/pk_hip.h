@@ -237,7 +237,9 @@ int pk_hip_layernorm_dev(float *x, uint32_t T, uint32_t n, const float *w, const
                          void *stream);
 
 /* The attention's float part (core/encoder.c:280-327): H heads of D / H
- * dimensions (a multiple of 64), o [T][D] from the products' outputs q, k,
+ * dimensions (a multiple of 16; heads of a multiple of 64 run on the
+ * tiled kernels, others on one thread an output), o [T][D] from the
+ * products' outputs q, k,
  * v [T][D] and the positions' p [2T - 1][D] with the biases u and v [D]:
  * Transformer-XL's scores, the softmax, the weighted values, each output
  * the chain pk_k_gemm_f32 and pk_k_softmax make. The scores live in ws,
@@ -261,7 +263,7 @@ int pk_hip_attention_noalloc_dev(float *o, const float *q, const float *k, const
 
 /* One encoder layer's weights on the device (core/model.h:45-53): the
  * eleven matrices uploaded, the vectors as device pointers. D = d_model
- * (a multiple of 64 up to 4096), H heads of D / H (a multiple of 64),
+ * (a multiple of 64 up to 4096), H heads of D / H (a multiple of 16),
  * F = ff_dim (a multiple of 64 up to 4096), K depthwise taps (<= 33). */
 typedef struct {
     uint32_t D, H, F, K;

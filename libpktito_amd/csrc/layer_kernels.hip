@@ -908,6 +908,50 @@ int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b
     return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
+/* Heads whose width is not a multiple of 64 (the tiled kernels' stage):
+ * one thread an output, the same chains in the same order. A score is the
+ * content chain fma(k, q + u) and the position chain fma(p_m, q + v) over
+ * the head's dimensions in order from +0, m = T - 1 - i + j, then their sum;
+ * an output is the chain fma(v_j, e_ij * (1 / sum_i)) over the T keys in
+ * order from +0. */
+__global__ __launch_bounds__(256) void att_scores_small_kernel(float *__restrict__ S, uint32_t Ts,
+                                                               const float *__restrict__ qf,
+                                                               const float *__restrict__ kf,
+                                                               const float *__restrict__ pf,
+                                                               const float *__restrict__ bu,
+                                                               const float *__restrict__ bv, uint32_t T,
+                                                               uint32_t D, uint32_t dk) {
+    const uint64_t id = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint32_t H = D / dk;
+    if (id >= (uint64_t)H * T * T)
+        return;
+    const uint32_t j = (uint32_t)(id % T), i = (uint32_t)(id / T % T), h = (uint32_t)(id / ((uint64_t)T * T));
+    const float *q = qf + (size_t)i * D + h * dk, *k = kf + (size_t)j * D + h * dk;
+    const float *p = pf + (size_t)(T - 1 - i + j) * D + h * dk, *u = bu + h * dk, *v = bv + h * dk;
+    float sc = 0.0f, bd = 0.0f;
+    for (uint32_t d = 0; d < dk; d++) {
+        sc = __builtin_fmaf(k[d], q[d] + u[d], sc);
+        bd = __builtin_fmaf(p[d], q[d] + v[d], bd);
+    }
+    S[((size_t)h * T + i) * Ts + j] = sc + bd;
+}
+
+__global__ __launch_bounds__(256) void att_pv_small_kernel(float *__restrict__ of, const float *__restrict__ S,
+                                                           const float *__restrict__ inv, uint32_t Ts,
+                                                           const float *__restrict__ vf, uint32_t T, uint32_t D,
+                                                           uint32_t dk) {
+    const uint64_t id = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= (uint64_t)T * D)
+        return;
+    const uint32_t d = (uint32_t)(id % D), i = (uint32_t)(id / D), h = d / dk;
+    const float *e = S + ((size_t)h * T + i) * Ts;
+    const float r = inv[(size_t)h * T + i];
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < T; j++)
+        acc = __builtin_fmaf(vf[(size_t)j * D + d], e[j] * r, acc);
+    of[(size_t)i * D + d] = acc;
+}
+
 /* The attention's kernels: 0 the matrix cores' (the default), 1 the VALU
  * chains; both compute the same bits. */
 static int g_att_valu = 0;
@@ -970,13 +1014,17 @@ int launch_attention(float *of, float *ws, const float *qf, const float *kf, con
                      int8_t *qp, float *qd, uint32_t qb) {
     if (T == 0)
         return 0;
-    if (H == 0 || D % H || (D / H) % 64 || (uint64_t)T * att_score_stride(T) >= (1ull << 32) - 1)
+    if (H == 0 || D % H || (D / H) % 16 || (uint64_t)T * att_score_stride(T) >= (1ull << 32) - 1)
         return -2;
-    if (qp && (g_att_valu || !(qb == 32 || qb == 64)))
+    const bool small = (D / H) % 64 != 0;
+    if (qp && (g_att_valu || small || !(qb == 32 || qb == 64)))
         return -2;                                  /* no quantizing epilogue there: nothing launched */
     const uint32_t dk = D / H, Ts = att_score_stride(T), tiles = (T + kAT - 1) / kAT, rows = H * T;
     float *S = ws, *inv = ws + (size_t)rows * Ts;
-    if (g_att_valu) {
+    if (small) {
+        const uint64_t n = (uint64_t)H * T * T;
+        att_scores_small_kernel<<<(uint32_t)((n + 255) / 256), 256, 0, s>>>(S, Ts, qf, kf, pf, bu, bv, T, D, dk);
+    } else if (g_att_valu) {
         att_scores_kernel<<<dim3(tiles, tiles, H), 256, 0, s>>>(S, Ts, qf, kf, pf, bu, bv, T, D, dk);
     } else {
         const uint32_t qt = (T + kSQ - 1) / kSQ;
@@ -990,7 +1038,9 @@ int launch_attention(float *of, float *ws, const float *qf, const float *kf, con
         att_softmax_reg_kernel<64><<<(rows + 15) / 16, 256, 0, s>>>(S, inv, Ts, rows, T, scale);
     else
         att_softmax_kernel<<<(rows + 15) / 16, 256, 0, s>>>(S, inv, Ts, rows, T, scale);
-    if (g_att_valu)
+    if (small)
+        att_pv_small_kernel<<<(uint32_t)(((uint64_t)T * D + 255) / 256), 256, 0, s>>>(of, S, inv, Ts, vf, T, D, dk);
+    else if (g_att_valu)
         att_pv_kernel<<<dim3(dk / kPD, (T + kPI - 1) / kPI, H), 128, 0, s>>>(of, S, inv, Ts, vf, T, D, dk);
     else
         att_pv_mfma_kernel<<<dim3((T + 63) / 64, dk / 64, H), 256, 0, s>>>(of, S, inv, Ts, vf, T, D, dk, qp, qd,

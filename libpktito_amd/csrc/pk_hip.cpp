@@ -909,9 +909,9 @@ int layer_check(const pk_hip_layer *L, uint32_t qb) {
     if (!L)
         return fail(PK_HIP_EINVAL, "layer_dev: no layer");
     const uint32_t D = L->D, F = L->F, H = L->H;
-    if (D == 0 || D % 64 || D > 4096 || F == 0 || F % 64 || F > 4096 || H == 0 || D % H || (D / H) % 64 ||
+    if (D == 0 || D % 64 || D > 4096 || F == 0 || F % 64 || F > 4096 || H == 0 || D % H || (D / H) % 16 ||
         L->K == 0 || L->K > 33 || !(qb == 32 || qb == 64) || !(L->eps >= 0.0f))
-        return fail(PK_HIP_EINVAL, "layer_dev: D and F multiples of 64 up to 4096, heads of a multiple of 64, "
+        return fail(PK_HIP_EINVAL, "layer_dev: D and F multiples of 64 up to 4096, heads of a multiple of 16, "
                                    "1 to 33 taps, blocks of 32 or 64");
     const float *v[] = { L->ff1_nw, L->ff1_nb, L->att_nw, L->att_nb, L->conv_nw, L->conv_nb, L->ff2_nw,
                          L->ff2_nb, L->out_nw, L->out_nb, L->bias_u, L->bias_v, L->dw_b };
@@ -1013,8 +1013,8 @@ int pk_hip_attention_dev(float *o, const float *q, const float *k, const float *
         return e;
     if (T == 0)
         return PK_HIP_OK;
-    if (!o || !q || !k || !v || !p || !bias_u || !bias_v || !ws || H == 0 || D % H || (D / H) % 64)
-        return fail(PK_HIP_EINVAL, "attention_dev: heads of a multiple of 64 dimensions, every pointer set");
+    if (!o || !q || !k || !v || !p || !bias_u || !bias_v || !ws || H == 0 || D % H || (D / H) % 16)
+        return fail(PK_HIP_EINVAL, "attention_dev: heads of a multiple of 16 dimensions, every pointer set");
     if (ws_bytes < pk_hip_attention_workspace(T, H))
         return fail(PK_HIP_EINVAL, "attention_dev: workspace of %zu bytes, %zu needed", ws_bytes,
                     pk_hip_attention_workspace(T, H));
@@ -1032,8 +1032,8 @@ int pk_hip_attention_noalloc_dev(float *o, const float *q, const float *k, const
         return e;
     if (T == 0)
         return PK_HIP_OK;
-    if (!o || !q || !k || !v || !p || !bias_u || !bias_v || H == 0 || D % H || (D / H) % 64)
-        return fail(PK_HIP_EINVAL, "attention_noalloc_dev: heads of a multiple of 64 dimensions, every pointer set");
+    if (!o || !q || !k || !v || !p || !bias_u || !bias_v || H == 0 || D % H || (D / H) % 16)
+        return fail(PK_HIP_EINVAL, "attention_noalloc_dev: heads of a multiple of 16 dimensions, every pointer set");
     const size_t need = pk_hip_attention_workspace(T, H);
     if (need > pkq8::kStaticScratchBytes)
         return fail(PK_HIP_EINVAL,

@@ -21,7 +21,8 @@
  * each layer's input and output, the positions' quantized encodings and
  * every layer's weights, for the oracle's layer to be compared with. Layout
  * (little-endian): "PKLD", u32 Te, D, H, F, K, qb, L; f32 eps; f32 x[L + 1]
- * [Te][D]; i8 ape_q[2Te - 1][D]; f32 ape_d[2Te - 1][D / qb]; then a layer:
+ * [Te][D]; i8 ape_q[2Te - 1][D]; f32 ape_d[2Te - 1][D / qb]; f32 pe[2Te - 1]
+ * [D] (the encodings before their quantize); then a layer:
  * f32 ff1_nw, ff1_nb, att_nw, att_nb, conv_nw, conv_nb, ff2_nw, ff2_nb,
  * out_nw, out_nb, bias_u, bias_v [D]; f32 dw [D][K]; f32 dw_b [D]; and
  * ff1_up, ff1_down, ff2_up, ff2_down, q, k, v, pos, o, pw1, pw2 each as u32
@@ -92,6 +93,7 @@ static int dump_layers(pk_model *m, pk_asr *a, const float *x, size_t n, const c
     const size_t R = 2 * (size_t)Te - 1;
     put(f, a->ape.q, R * D);
     put(f, a->ape.d, R * (D / a->ape.qb) * sizeof(float));
+    put(f, a->pe, R * D * sizeof(float));
     for (uint32_t l = 0; l < L; l++) {
         const pk_layer *y = &m->layers[l];
         const float *vec[] = { y->ff1_nw, y->ff1_nb, y->att_nw, y->att_nb, y->conv_nw, y->conv_nb,

@@ -132,13 +132,15 @@ def test_dwq(hip, torch, T, D, K, qb):
 
 @pytest.mark.parametrize("valu", [0, 1])
 @pytest.mark.parametrize("T,D,H", [(1, 128, 2), (2, 128, 2), (7, 64, 1), (17, 128, 2), (64, 128, 2), (65, 256, 2),
-                                   (130, 128, 2), (100, 1024, 8), (289, 128, 1)])
+                                   (130, 128, 2), (100, 1024, 8), (289, 128, 1),
+                                   (37, 64, 4), (50, 128, 4), (9, 96, 2), (300, 64, 4)])
 def test_attention(hip, torch, T, D, H, valu):
     """The attention's scores (with the positions' diagonals), softmax and
     weighted values against pk_k_gemm_f32 and pk_k_softmax composed on the
     CPU with the reference's panel layouts; on the matrix cores (one-step
     MFMAs) and as VALU chains. T covers one key, partial tiles and bands,
-    and key counts that are not multiples of 8."""
+    and key counts that are not multiples of 8; heads of 16, 32 and 48
+    dimensions run on the one-thread-an-output kernels."""
     g = synth.rng(T * 7 + D)
     q, k, v = (g.standard_normal((3, T, D)) * 1.5).astype(np.float32)
     p = g.standard_normal((2 * T - 1, D)).astype(np.float32)
@@ -223,6 +225,15 @@ def run_layer(hip, torch, D, H, F, K, T, qb, seed, threads=16, tweak=None):
     want = ol.conformer_layer(w, x, T, ape_q, ape_d, qb, threads=threads)
     assert np.all(np.isfinite(want))
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("T,qb", [(1, 32), (37, 64), (88, 32)])
+def test_layer_small_heads(hip, torch, T, qb):
+    """d_model 64 in 4 heads of 16, ff 128, 9 taps (the reference's tiny
+    model's shapes): the attention on its one-thread-an-output kernels, its
+    output quantized by a pass of its own; the whole layer against the
+    oracle's."""
+    run_layer(hip, torch, D=64, H=4, F=128, K=9, T=T, qb=qb, seed=900 + T)
 
 
 @pytest.mark.parametrize("valu", [0, 1])

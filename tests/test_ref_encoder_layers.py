@@ -1,4 +1,4 @@
-"""The oracle's encoder layer against the reference's own.
+"""The oracle's and the device's encoder layer against the reference's own.
 
 oracle/Makefile builds the reference's library where its files lie, with
 the harness oracle/dropin_cli.c, which runs the reference's encoder
@@ -12,7 +12,8 @@ the reference's output bits, for both layers and in both of the encoder's
 block sizes (32, and 64 in its fast mode). This pins the oracle's
 composition of the layer (the order of its passes, which activation each
 product reads, where the residuals add) to the reference's encoder itself,
-not to a second restatement. CPU only: the hip table is not used."""
+not to a second restatement; and the device-resident layer
+(pk_hip_layer_dev) to the same outputs, on the GPU."""
 import os
 import subprocess
 
@@ -47,6 +48,7 @@ def read_dump(path):
     R = 2 * Te - 1
     ape_q = take(np.int8, R * D)
     ape_d = take(np.float32, R * (D // qb))
+    pe = take(np.float32, R * D).reshape(R, D)
     layers = []
     for _ in range(L):
         w = dict(D=D, H=H, F=F, K=K, eps=eps)
@@ -60,11 +62,10 @@ def read_dump(path):
             w[n + "_s"] = take(np.float32, rows)
         layers.append(w)
     assert off == len(raw)
-    return dict(Te=Te, qb=qb, xs=xs, ape_q=ape_q, ape_d=ape_d, layers=layers)
+    return dict(Te=Te, qb=qb, xs=xs, ape_q=ape_q, ape_d=ape_d, pe=pe, layers=layers)
 
 
-@pytest.mark.parametrize("fast", [0, 1])
-def test_oracle_layer_is_the_reference_encoders(tmp_path, fast):
+def reference_layers(tmp_path, fast):
     if not os.path.exists(CLI):
         pytest.skip("oracle/_ref/dropin_cli was not built (the reference checkout was absent when build() ran)")
     out = tmp_path / "layers.bin"
@@ -73,7 +74,12 @@ def test_oracle_layer_is_the_reference_encoders(tmp_path, fast):
                        env=env, timeout=300)
     assert r.returncode == 0, r.stderr[-2000:]
     assert "ref" in r.stderr.split("backend:")[-1]
-    dump = read_dump(out)
+    return read_dump(out)
+
+
+@pytest.mark.parametrize("fast", [0, 1])
+def test_oracle_layer_is_the_reference_encoders(tmp_path, fast):
+    dump = reference_layers(tmp_path, fast)
     assert dump["qb"] == (64 if fast else 32) and len(dump["layers"]) == 2
     Te = dump["Te"]
     for i, w in enumerate(dump["layers"]):
@@ -81,3 +87,43 @@ def test_oracle_layer_is_the_reference_encoders(tmp_path, fast):
         assert np.isfinite(want).all() and not np.array_equal(bits(x_in), bits(want))
         got = ol.conformer_layer(w, x_in, Te, dump["ape_q"], dump["ape_d"], dump["qb"], threads=4)
         assert np.array_equal(bits(got), bits(want)), (fast, i)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("valu", [0, 1])
+@pytest.mark.parametrize("fast", [0, 1])
+def test_device_layer_is_the_reference_encoders(hip, tmp_path, fast, valu):
+    """pk_hip_layer_dev (the whole layer in HBM) on the same input, the
+    reference's positional encodings quantized on the device (which must
+    give the reference's bytes and scales) and the same weights: the
+    reference's output bits, for both layers. The tiny model's heads are 16
+    wide, so the attention runs on its one-thread-an-output kernels (whose
+    output is quantized by a pass of its own) whatever valu sets."""
+    import torch
+    dump = reference_layers(tmp_path, fast)
+    Te, qb = dump["Te"], dump["qb"]
+    D = dump["layers"][0]["D"]
+    R = 2 * Te - 1
+    ape_q = torch.empty((R, D), dtype=torch.int8, device="cuda")
+    ape_qp = torch.zeros((hip.packed_bytes(D, R),), dtype=torch.int8, device="cuda")
+    ape_d = torch.empty((R * (D // qb),), dtype=torch.float32, device="cuda")
+    hip.quantize_packed_dev(ape_q, ape_qp, ape_d, torch.from_numpy(dump["pe"]).cuda(), D, R, D, qb=qb)
+    torch.cuda.synchronize()
+    assert np.array_equal(ape_q.cpu().numpy().reshape(-1), dump["ape_q"])
+    assert np.array_equal(bits(ape_d.cpu().numpy()), bits(dump["ape_d"]))
+    was = hip.force_attention(valu)
+    try:
+        for i, w in enumerate(dump["layers"]):
+            lay = hip.DeviceLayer(w, torch)
+            try:
+                ws = torch.empty((lay.workspace(Te, qb),), dtype=torch.uint8, device="cuda")
+                xt = torch.from_numpy(np.ascontiguousarray(dump["xs"][i])).cuda()
+                print("[case] device layer", fast, valu, i, flush=True)
+                lay.run(xt, Te, ape_qp, ape_d, qb, ws)
+                torch.cuda.synchronize()
+                got = xt.cpu().numpy()
+            finally:
+                lay.release()
+            assert np.array_equal(bits(got), bits(dump["xs"][i + 1])), (fast, valu, i)
+    finally:
+        hip.force_attention(was)
