@@ -36,8 +36,9 @@
  * (core/decoder.c:121-147). Layout: "PKDC", u32 Te, P, L, J, V, n_dur,
  * blank, max_symbols, dur[n_dur]; f32 f[Te][J]; f32 embed[V + 1][P]; per
  * LSTM layer wx, wh (u32 rows, cols, i8 panels, f32 scales) and f32 b[4P];
- * jpred, f32 jpred_b[J]; jout, f32 jout_b[its rows]; u32 ntoks; i32 (id,
- * frame, dur) a token. */
+ * jpred, f32 jpred_b[J]; jout, f32 jout_b[its rows]; jenc, f32 jenc_b[J]
+ * (the joint's encoder half, f's product); u32 ntoks; i32 (id, frame, dur)
+ * a token. */
 #include "pktito.h"
 #include "model.h"
 #include "asr.h"
@@ -132,6 +133,8 @@ static int dump_decoder(const pk_model *m, const pk_asr *a, uint32_t Te, const c
     put(f, m->jpred_b, (size_t)J * sizeof(float));
     put_q8(f, &m->jout);
     put(f, m->jout_b, (size_t)m->jout.rows * sizeof(float));
+    put_q8(f, &m->jenc);
+    put(f, m->jenc_b, (size_t)J * sizeof(float));
     put_u32(f, (uint32_t)a->ntoks);
     for (size_t i = 0; i < a->ntoks; i++) {
         const int32_t t3[3] = { a->toks[i].id, a->toks[i].frame, a->toks[i].dur };

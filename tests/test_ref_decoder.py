@@ -54,14 +54,17 @@ def read_dump(path):
     dec["jpred_b"] = take(np.float32, J)
     rows = q8(dec, "jout")
     dec["jout_b"] = take(np.float32, rows)
+    jenc = {}
+    q8(jenc, "jenc")
+    jenc["jenc_b"] = take(np.float32, J)
     n = int(take(np.uint32, 1)[0])
     toks = [tuple(int(v) for v in take(np.int32, 3)) for _ in range(n)]
     assert off == len(raw)
-    return dict(Te=Te, f=f, dec=dec, blank=blank, durs=durs, max_symbols=max_symbols, toks=toks)
+    return dict(Te=Te, f=f, dec=dec, jenc=jenc, blank=blank, durs=durs, max_symbols=max_symbols, toks=toks)
 
 
-@pytest.mark.parametrize("seconds,seed,fast", [(7, 3, 0), (20, 1, 0), (20, 2, 1)])
-def test_oracle_decoder_is_the_references(tmp_path, seconds, seed, fast):
+def reference_decoder(tmp_path, seconds, seed, fast):
+    """(the dump, the harness's stdout) of a transcription on ref"""
     if not os.path.exists(CLI):
         pytest.skip("oracle/_ref/dropin_cli was not built (the reference checkout was absent when build() ran)")
     out = tmp_path / "decoder.bin"
@@ -69,7 +72,12 @@ def test_oracle_decoder_is_the_references(tmp_path, seconds, seed, fast):
     r = subprocess.run([CLI, TINY, str(seconds), str(seed), str(fast), "8", "--decoder", str(out)],
                        capture_output=True, text=True, env=env, timeout=300)
     assert r.returncode == 0, r.stderr[-2000:]
-    d = read_dump(out)
+    return read_dump(out), r.stdout
+
+
+@pytest.mark.parametrize("seconds,seed,fast", [(7, 3, 0), (20, 1, 0), (20, 2, 1)])
+def test_oracle_decoder_is_the_references(tmp_path, seconds, seed, fast):
+    d, stdout = reference_decoder(tmp_path, seconds, seed, fast)
     dec = d["dec"]
     dw = ol.DecoderWeights(dec)
     st = {"h": np.zeros((dec["L"], dec["P"]), np.float32), "c": np.zeros((dec["L"], dec["P"]), np.float32),
@@ -85,7 +93,7 @@ def test_oracle_decoder_is_the_references(tmp_path, seconds, seed, fast):
     assert len(d["toks"]) > 5
     assert got == d["toks"]
     # and the transcript the harness printed is the same search's
-    printed = [tuple(int(v) for v in line.split()) for line in r.stdout.splitlines()[1:]]
+    printed = [tuple(int(v) for v in line.split()) for line in stdout.splitlines()[1:]]
     assert printed == d["toks"]
 
 
@@ -96,14 +104,7 @@ def test_device_decoder_is_the_references(hip, tmp_path, seconds, seed, fast):
     the jpred gemv, in DeviceDecoder) driving the same search over the
     reference's joint frames of tiny.pkf: the reference's tokens."""
     import torch
-    if not os.path.exists(CLI):
-        pytest.skip("oracle/_ref/dropin_cli was not built (the reference checkout was absent when build() ran)")
-    out = tmp_path / "decoder.bin"
-    env = dict(os.environ, PKTITO_KERNELS="ref")
-    r = subprocess.run([CLI, TINY, str(seconds), str(seed), str(fast), "8", "--decoder", str(out)],
-                       capture_output=True, text=True, env=env, timeout=300)
-    assert r.returncode == 0, r.stderr[-2000:]
-    d = read_dump(out)
+    d, _ = reference_decoder(tmp_path, seconds, seed, fast)
     dd = hip.DeviceDecoder(d["dec"], torch)
     try:
         fd = torch.from_numpy(np.ascontiguousarray(d["f"])).cuda()
