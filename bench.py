@@ -77,6 +77,8 @@ def parse():
                    help="only M-row products through rotated K x N matrices, 50 launches (for rocprofv3)")
     p.add_argument("--profile-decoder", action="store_true",
                    help="the decoder's token steps only (graphs of a prediction and a joint, no CPU leg)")
+    p.add_argument("--peaks", action="store_true",
+                   help="only the on-machine check of the int8 MFMA and HBM read peaks")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only copy 256 MiB three times (the known-size kernel that scales "
                         "rocprofv3's FETCH_SIZE / WRITE_SIZE)")
@@ -385,6 +387,42 @@ def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20, rows=(1, 4, 16), lau
             m.release()
         del big, rot
     return out
+
+
+def peak_check(pk, torch):
+    """The two published peaks the rooflines divide by, checked on this
+    machine: the int8 matrix cores' rate (2048 workgroups of four waves, each
+    wave 4096 rounds of eight independent 16x16x64 MFMAs on registers, 32768
+    ops an MFMA), and a streaming read of 4 GiB (ten times the 256 MB MALL).
+    Each is the best of three launches timed with events on the current
+    stream, the stream the launches go to."""
+    sink = torch.zeros((4,), dtype=torch.int32, device="cuda")
+    wgs, iters = 2048, 4096
+    ops = wgs * 4 * iters * 8 * 32768
+
+    def best(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return min(ts)
+    mms = best(lambda: pk.mfma_rate_dev(wgs, iters, sink))
+    buf = torch.empty((4 << 30,), dtype=torch.uint8, device="cuda")
+    buf.random_(0, 256)
+    rms = best(lambda: pk.stream_read_dev(buf, sink))
+    del buf
+    torch.cuda.empty_cache()
+    tops = ops / (mms * 1e-3) / 1e12
+    gbs = (4 << 30) / (rms * 1e-3) / 1e9
+    return dict(mfma_int8_tops=round(tops, 1), of_published_mfma=round(tops / MFMA_INT8_PEAK_TOPS, 3),
+                hbm_read_GBs=round(gbs, 1), of_published_hbm=round(gbs / HBM_PEAK_GBS, 3),
+                mfma_ms=round(mms, 3), read_ms=round(rms, 3))
 
 
 # --------------------------------------------------------- CPU baseline ---
@@ -751,6 +789,9 @@ def main():
     torch.cuda.set_device(0)
 
     M = 750
+    if args.peaks:
+        print(json.dumps({"peaks_measured": peak_check(pk, torch)}))
+        return
     if args.profile_decoder:
         print(json.dumps({"profiled": "decoder_steps", **decoder_steps(pk, torch, False)}))
         return
@@ -822,6 +863,10 @@ def main():
     release(layers)
     del layers, fn
     torch.cuda.empty_cache()
+
+    if not args.quick:
+        extra["peaks_measured"] = peak_check(pk, torch)
+        log(f"peaks: {extra['peaks_measured']}")
 
     if not args.quick:
         # the same sweep at one minute of audio

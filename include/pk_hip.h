@@ -323,12 +323,19 @@ int pk_hip_joint_dev(float *logit, uint32_t *tok_dur, const pk_hip_q8 *jout, con
 /* Measurement aids, with no counterpart in the reference: the floors a
  * small product's time is read against. pk_hip_empty_dev launches an empty
  * kernel; pk_hip_stream_read_dev reads the bytes at p (16-byte aligned,
- * bytes a multiple of 16) with one 16-byte load a thread over as many
- * workgroups as they need, and writes *sink only if the loads' fold meets a
+ * bytes a multiple of 16) with non-temporal 16-byte loads, one a thread
+ * over as many workgroups as they need (at most 32768, four loads a thread
+ * in flight beyond that), and writes *sink only if the loads' fold meets a
  * fixed constant (so nothing is written in practice; sink is device
  * memory). */
 int pk_hip_empty_dev(void *stream);
 int pk_hip_stream_read_dev(const void *p, size_t bytes, uint32_t *sink, void *stream);
+/* A measurement aid with no counterpart in the reference: the int8 matrix
+ * cores' rate, for checking the published peak on the machine.
+ * workgroups of four waves each run iters rounds of eight independent
+ * v_mfma_i32_16x16x64_i8 (32768 ops each) on registers, nothing loaded;
+ * *sink as for pk_hip_stream_read_dev. */
+int pk_hip_mfma_rate_dev(uint32_t workgroups, uint32_t iters, uint32_t *sink, void *stream);
 
 /* The kernel variant the calling thread launched last, for profiling and
  * tests. */

@@ -125,6 +125,7 @@ _SIGS = {
                              [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "pk_hip_empty_dev": (ctypes.c_int, [ctypes.c_void_p]),
     "pk_hip_stream_read_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]),
+    "pk_hip_mfma_rate_dev": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]),
     "pk_hip_attention_noalloc_dev": (ctypes.c_int, [ctypes.c_void_p] * 7 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]),
     "pk_hip_layer_workspace": (ctypes.c_size_t, [ctypes.POINTER(LayerW), ctypes.c_uint32, ctypes.c_uint32]),
     "pk_hip_gemv_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -406,6 +407,12 @@ def stream_read_dev(buf, sink, nbytes=None, stream=None):
     measurements)."""
     n = buf.numel() * buf.element_size() if nbytes is None else nbytes
     _check(lib().pk_hip_stream_read_dev(_dptr(buf), n, _dptr(sink), _stream(stream)))
+
+
+def mfma_rate_dev(workgroups, iters, sink, stream=None):
+    """workgroups x 4 waves x iters x 8 int8 16x16x64 MFMAs (32768 ops each)
+    on registers: the matrix cores' rate, for measurements."""
+    _check(lib().pk_hip_mfma_rate_dev(workgroups, iters, _dptr(sink), _stream(stream)))
 
 
 class DeviceLayer:

@@ -1,8 +1,9 @@
-/* Measurement aids: the floors a small product's time is read against. An
- * empty kernel (the cost of a launch), and a streaming read of a buffer by
- * one 16-byte load a thread over as many workgroups as the bytes need, every
- * load in flight at once, folded so that none is dropped; nothing is written
- * unless the fold meets a fixed 32-bit constant. */
+/* Measurement aids: the floors a small product's time is read against and
+ * the rates the peaks are checked with on the machine. An empty kernel (the
+ * cost of a launch); a streaming read of a buffer over as many workgroups
+ * as its 16-byte pieces need (one a thread, at most 32768 workgroups),
+ * folded so that none is dropped; and the int8 matrix cores' rate.
+ * Nothing is written unless a fold meets a fixed 32-bit constant. */
 #include "pk_hip.h"
 #include "q8_internal.h"
 
@@ -10,15 +11,65 @@ namespace pkq8 {
 
 __global__ __launch_bounds__(256) void empty_kernel() {}
 
-__global__ __launch_bounds__(256) void stream_read_kernel(const uint4 *__restrict__ p, uint64_t n16,
+typedef unsigned int v4u_d __attribute__((ext_vector_type(4)));
+
+/* Grid-stride, four non-temporal 16-byte loads in flight a thread a round
+ * (the form that read fastest on the machine), then the rest one at a time;
+ * every index is below n16 by the loop bounds. */
+__global__ __launch_bounds__(256) void stream_read_kernel(const v4u_d *__restrict__ p, uint64_t n16,
                                                           uint32_t *__restrict__ sink) {
     uint32_t f = 0;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256) {
-        const uint4 v = p[i];
+    const uint64_t step = (uint64_t)gridDim.x * 256;
+    uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * step < n16; i += 4 * step) {
+        v4u_d v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            v[u] = __builtin_nontemporal_load(p + i + u * step);
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            f ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += step) {
+        const v4u_d v = __builtin_nontemporal_load(p + i);
         f ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     if (f == 0x9E3779B9u)
         *sink = f;
+}
+
+/* The matrix cores' rate: every wave runs iters rounds of eight
+ * independent v_mfma_i32_16x16x64_i8 chains on operands held in registers
+ * (nothing loaded in the loop); the sums are folded and written only if they
+ * meet a fixed constant. 32768 ops an MFMA. */
+typedef int v4i_d __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void mfma_rate_kernel(uint32_t iters, uint32_t seed, uint32_t *__restrict__ sink) {
+    const int lane = threadIdx.x & 63;
+    v4i_d a = { (int)(seed ^ lane), (int)(seed + lane), (int)(seed * 3u), (int)lane };
+    v4i_d b = { (int)(seed + 7u), (int)(lane * 5), (int)(seed ^ 0x55u), (int)(seed - lane) };
+    v4i_d acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+        acc[c] = v4i_d{ c, 0, 0, 0 };
+    for (uint32_t i = 0; i < iters; i++) {
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[c], 0, 0, 0);
+    }
+    int f = 0;
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+        f ^= acc[c][0] ^ acc[c][1] ^ acc[c][2] ^ acc[c][3];
+    if ((uint32_t)f == 0x9E3779B9u)
+        *sink = (uint32_t)f;
+}
+
+int launch_mfma_rate(uint32_t workgroups, uint32_t iters, uint32_t *sink, hipStream_t s) {
+    if (workgroups == 0 || iters == 0)
+        return 0;
+    mfma_rate_kernel<<<workgroups, 256, 0, s>>>(iters, workgroups * 2654435761u, sink);
+    return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_empty(hipStream_t s) {
@@ -31,7 +82,7 @@ int launch_stream_read(const void *p, uint64_t bytes, uint32_t *sink, hipStream_
     if (n16 == 0)
         return 0;
     const uint64_t wg = (n16 + 255) / 256;
-    stream_read_kernel<<<(uint32_t)(wg < 8192 ? wg : 8192), 256, 0, s>>>((const uint4 *)p, n16, sink);
+    stream_read_kernel<<<(uint32_t)(wg < 32768 ? wg : 32768), 256, 0, s>>>((const v4u_d *)p, n16, sink);
     return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 

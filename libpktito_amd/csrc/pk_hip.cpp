@@ -1223,4 +1223,15 @@ int pk_hip_stream_read_dev(const void *p, size_t bytes, uint32_t *sink, void *st
     return PK_HIP_OK;
 }
 
+int pk_hip_mfma_rate_dev(uint32_t workgroups, uint32_t iters, uint32_t *sink, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!sink)
+        return fail(PK_HIP_EINVAL, "mfma_rate_dev: sink is NULL");
+    PK_LAUNCH(pkq8::launch_mfma_rate(workgroups, iters, sink, (hipStream_t)stream), "mfma rate launch");
+    g_kernel = "mfma_rate";
+    return PK_HIP_OK;
+}
+
 }  // extern "C"

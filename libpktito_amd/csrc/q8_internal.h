@@ -156,6 +156,8 @@ int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstr
  * bytes (a multiple of 16) at p, 16-byte aligned. */
 int launch_empty(hipStream_t s);
 int launch_stream_read(const void *p, uint64_t bytes, uint32_t *sink, hipStream_t s);
+/* workgroups of four waves, each iters rounds of eight int8 16x16x64 MFMAs */
+int launch_mfma_rate(uint32_t workgroups, uint32_t iters, uint32_t *sink, hipStream_t s);
 
 /* One product; table->nseg == 1 for a plain call. With g.oqp set, -3 where
  * the fused SiLU quantize is not available (nothing launched). */
