@@ -353,8 +353,8 @@ int pk_hip_force_tiling(int index);
 
 /* Tests and tuning: forcing the packed quantize's kernel for every later
  * launch in the process: 0 one wave a column (or a wave a 1024-input chunk
- * of a column over 1024 inputs in blocks), 1 one workgroup a 16-column
- * group, 2 one wave a whole column, -1 the automatic choice by size;
+ * of a column over 1024 inputs in blocks), 1 one workgroup a half
+ * 16-column group, 2 one wave a whole column, -1 the automatic choice by size;
  * returns the one forced before. All compute the same bits. */
 int pk_hip_force_quantize(int kind);
 

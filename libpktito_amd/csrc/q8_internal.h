@@ -104,7 +104,7 @@ const char *ring_name(int i);
 int set_ring(int i);
 
 /* The packed quantize's kernel: 0 one wave a column (a wave a 1024-input
- * chunk of a wide column in blocks), 1 one workgroup a group, 2 one wave a
+ * chunk of a wide column in blocks), 1 one workgroup a half group, 2 one wave a
  * whole column, -1 by size; returns the one forced before. */
 int set_quant_kernel(int kind);
 

@@ -232,10 +232,19 @@ int launch_quantize_directed(int8_t *q, float *d, const float *x, size_t xs, uin
 }
 
 /* One wave a column of n <= 4096 inputs, four columns a workgroup (the
- * quantizes of up to about 7M inputs, where the kernel is one memory round
+ * quantizes of up to 5-9M inputs, where the kernel is one memory round
  * trip and wants its loads spread over the most CUs). */
 /* What a quantize does to its inputs first: nothing, or SiLU (the feed-
  * forward's hidden activations, core/encoder.c:147-156). */
+/* A quantize reads each input once: non-temporal loads keep them from
+ * pushing the products' weights and activations out of the caches (the
+ * 24-layer chain at 7500 frames: 11.43 -> 11.09 ms). */
+typedef float v4f_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ntload4(const float4 *p) {
+    const v4f_nt t = __builtin_nontemporal_load((const v4f_nt *)p);
+    return make_float4(t.x, t.y, t.z, t.w);
+}
+
 template <int OP>
 __device__ __forceinline__ float4 quant_in(float4 v) {
     if constexpr (OP == kOpSilu)
@@ -258,7 +267,7 @@ __global__ __launch_bounds__(256) void quant_wave_kernel(int8_t *__restrict__ q,
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
-        v[c] = i < n4 ? quant_in<OP>(xr[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[c] = i < n4 ? quant_in<OP>(ntload4(xr + i)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     const WaveScales<CH, QB> sc(v);
     int *qr = (int *)(q + (size_t)t * n);
@@ -304,7 +313,7 @@ __global__ __launch_bounds__(256) void quant_chunk_kernel(int8_t *__restrict__ q
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const uint32_t i = i0 + lane + 64 * c;
-        v[c] = i < n4 ? quant_in<OP>(xr[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[c] = i < n4 ? quant_in<OP>(ntload4(xr + i)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     const WaveScales<4, QB> sc(v);
     int *qr = (int *)(q + (size_t)t * n);
@@ -324,22 +333,26 @@ __global__ __launch_bounds__(256) void quant_chunk_kernel(int8_t *__restrict__ q
     }
 }
 
-/* One workgroup of 16 waves a group of 16 columns, for the packed copy of
- * about 7M inputs and more: wave r quantizes column 16 g + r as
- * quant_wave_kernel does, the group's units are put together in LDS, and
- * each unit leaves as one contiguous 1 KB of 16-byte stores (measured on
- * inputs the caches no longer hold: 10% sooner than the 4-byte stores at
- * these sizes, which are bound by HBM). The stores are ordinary ones: the
- * product that reads the copy next finds it in the memory-side cache, and
- * a layer of ten minutes of audio took 2% longer with non-temporal stores.
- * Columns past T are written as zero rows of the group. */
+/* The packed copy of 5-9M inputs and more: half a 16-column group a
+ * workgroup, 8 columns, a wave each quantizing its column as
+ * quant_wave_kernel does (512 threads, so two workgroups fit a CU and one's
+ * loads run under the other's stores). Workgroup b takes group b / 2,
+ * columns 8 (b % 2) .. + 7; their bytes meet in LDS, and each quarter of
+ * each unit holds the 8 columns' 16-byte pieces side by side, so the
+ * workgroup writes whole 128-byte lines with 16-byte stores (7500 x 4096:
+ * a whole group a 1024-thread workgroup 32.2 us, this 27.7 us, a quarter
+ * group of half lines 30.9 us; 4-byte stores, quant_wave_kernel's, are
+ * slower still at these sizes, which are bound by HBM). The stores are
+ * ordinary ones: the product that reads the copy next finds it in the
+ * memory-side cache (a layer of ten minutes of audio took 2% longer with
+ * non-temporal stores). Columns past T are written as zero rows. */
 template <int CH, int QB, int OP = kOpPlain>
-__global__ __launch_bounds__(1024) void quant_group_kernel(int8_t *__restrict__ q, int8_t *__restrict__ qp,
-                                                           float *__restrict__ d, const float *__restrict__ x,
-                                                           size_t xs, uint32_t n, uint32_t T) {
-    __shared__ __attribute__((aligned(16))) int8_t units[CH * 4 * kUnitBytes];
-    const int lane = threadIdx.x & 63, r = threadIdx.x >> 6;
-    const uint32_t g = blockIdx.x, G = gridDim.x, t = 16 * g + r;
+__global__ __launch_bounds__(512) void quant_group_kernel(int8_t *__restrict__ q, int8_t *__restrict__ qp,
+                                                          float *__restrict__ d, const float *__restrict__ x,
+                                                          size_t xs, uint32_t n, uint32_t T) {
+    __shared__ __attribute__((aligned(16))) int8_t units[CH * 4 * kUnitBytes / 2];
+    const int lane = threadIdx.x & 63, rr = threadIdx.x >> 6;
+    const uint32_t g = blockIdx.x >> 1, h = blockIdx.x & 1, G = (T + 15) / 16, t = 16 * g + 8 * h + rr;
     const uint32_t n4 = n >> 2, nw = 16 * ((n + 63) / 64);     /* 4-byte words a frame's units hold */
     const bool live = t < T;
     const float4 *xr = (const float4 *)(x + (size_t)(live ? t : 0) * xs);
@@ -347,7 +360,7 @@ __global__ __launch_bounds__(1024) void quant_group_kernel(int8_t *__restrict__ 
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t i = lane + 64 * c;
-        v[c] = live && i < n4 ? quant_in<OP>(xr[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[c] = live && i < n4 ? quant_in<OP>(ntload4(xr + i)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     const WaveScales<CH, QB> sc(v);
     int *qr = (int *)(q + (size_t)t * n);
@@ -358,7 +371,9 @@ __global__ __launch_bounds__(1024) void quant_group_kernel(int8_t *__restrict__ 
         if (i < nw) {
             const bool in = live && i < n4;
             const int v4 = !in || sc.zero[cb] ? 0 : pack4(v[c], sc.id[cb]);
-            *(int *)(units + (i >> 4) * kUnitBytes + in_unit(4 * i, r)) = v4;
+            /* piece (unit k / 64, quarter (k / 16) % 4, column rr) */
+            const uint32_t k = 4 * i;
+            *(int *)(units + (((k >> 6) * 4 + ((k >> 4) & 3)) * 8 + rr) * 16 + (k & 15)) = v4;
             if (in && q)
                 qr[i] = v4;
             if (QB && in && (i & (QB / 4 - 1)) == 0)
@@ -368,18 +383,22 @@ __global__ __launch_bounds__(1024) void quant_group_kernel(int8_t *__restrict__ 
     if (QB == 0 && live && lane == 0)
         d[t] = sc.dv[0];
     __syncthreads();
-    for (uint32_t j = threadIdx.x; j < 4 * nw; j += 1024) {
-        const uint32_t u = j >> 6;
+    /* 32 pieces a unit: quarter w / 8, column 8 h + w % 8 of the group */
+    for (uint32_t j = threadIdx.x; j < 2 * nw; j += 512) {
+        const uint32_t u = j >> 5, w = j & 31;
         const v4i val = *(const v4i *)(units + 16 * j);
-        *(v4i *)(qp + ((size_t)u * G + g) * kUnitBytes + 16 * (j & 63)) = val;
+        *(v4i *)(qp + ((size_t)u * G + g) * kUnitBytes + ((w >> 3) * 16 + 8 * h + (w & 7)) * 16) = val;
     }
 }
 
-/* The packed quantize's kernel by size: one wave a column below about 7M
- * inputs, one workgroup a group from there (the crossover measured on
- * inputs the caches no longer hold: 6.1M inputs are sooner the first way,
- * 7.7M the second). */
-constexpr uint64_t kGroupQuantInputs = 7ull << 20;
+/* The packed quantize's kernel by size: one wave a column below a number of
+ * inputs, one workgroup a half group from there. The crossover, measured on
+ * inputs the caches no longer hold, falls with the width: 1024 wide, 4.4M
+ * inputs are sooner the first way and 5.9M the second; 4096 wide, 7.8M the
+ * first and 11.7M the second. */
+inline bool group_quantize(uint32_t n, uint32_t T) {
+    return (uint64_t)T * n >= (n > 1024 ? 9ull << 20 : 5ull << 20);
+}
 static int g_quant_kernel = -1;
 
 int set_quant_kernel(int kind) {
@@ -393,13 +412,13 @@ static int launch_quantize_packed_op(int8_t *q, int8_t *qp, float *d, const floa
                                      uint32_t qb, uint32_t T, hipStream_t s, const char **name) {
     const uint32_t n4 = n / 4;
     const bool small = n4 <= 256;
-    const bool group = g_quant_kernel < 0 ? (uint64_t)T * n >= kGroupQuantInputs : g_quant_kernel == 1;
+    const bool group = g_quant_kernel < 0 ? group_quantize(n, T) : g_quant_kernel == 1;
     /* 2: one wave a whole column also where the column is wide and in blocks */
     const bool wide = !small && !group && g_quant_kernel != 2;
 #define PK_QP(CH, QB, NAME)                                                                       \
     do {                                                                                          \
         if (group) {                                                                              \
-            quant_group_kernel<CH, QB, OP><<<(T + 15) / 16, 1024, 0, s>>>(q, qp, d, x, xs, n, T);    \
+            quant_group_kernel<CH, QB, OP><<<2 * ((T + 15) / 16), 512, 0, s>>>(q, qp, d, x, xs, n, T);   \
             *name = OP ? "quant_group_packed_silu" NAME : "quant_group_packed" NAME;                                                    \
         } else {                                                                                  \
             quant_wave_kernel<CH, true, QB, OP><<<(T + 3) / 4, 256, 0, s>>>(q, qp, d, x, xs, n, T);  \

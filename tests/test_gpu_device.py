@@ -337,8 +337,8 @@ def special_rows(x):
                                     (1800, 4096, 32), (7500, 1024, 1024), (2249, 4096, 64)])
 def test_packed_quantize_kernels(hip, torch, T, n, qb):
     """The packed quantize kernels (one wave a column, or a wave a
-    1024-input chunk of a wide column in blocks; one workgroup a 16-column
-    group) and the
+    1024-input chunk of a wide column in blocks; one workgroup a half
+    16-column group) and the
     choice by size: q, d and the packed bytes are
     the oracle's, with and without the row-major copy, over a packed buffer
     that held other bytes before."""
@@ -347,7 +347,7 @@ def test_packed_quantize_kernels(hip, torch, T, n, qb):
     q, d = ol.quantize(x.reshape(-1), T, n, qb, n)
     dev = torch.device("cuda")
     xt = torch.from_numpy(x).to(dev)
-    big = T * n >= 7 << 20
+    big = T * n >= (9 << 20 if n > 1024 else 5 << 20)
     try:
         for kind in (-1, 0, 1, 2):
             hip.force_quantize(kind)
