@@ -822,7 +822,9 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
     /* the wave's units u = wave + KW i, CU of them loaded at once (every
      * load of a batch issued before its first MFMA: one memory round trip a
      * batch, one batch for K <= 64 CU KW inputs); two accumulators so that
-     * consecutive MFMAs do not wait on each other (exact int32 sums) */
+     * consecutive MFMAs do not wait on each other (exact int32 sums). The
+     * weights, read once a call, load non-temporally: 8-11% sooner from
+     * HBM (weights rotated over > 512 MB), the same when they are cached. */
     constexpr int CU = 8;
     v4i acc[2] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
     for (uint32_t u0 = wave; u0 < kr; u0 += CU * KW) {
@@ -832,7 +834,7 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
             const uint32_t u = u0 + i * KW;
             if (u < kr) {
                 const uint32_t k = u * 64 + (lane >> 4) * 16;
-                wv[i] = *(const v4i *)(wp + (size_t)u * ws_);
+                wv[i] = __builtin_nontemporal_load((const v4i *)(wp + (size_t)u * ws_));
                 av[i] = *(const v4i *)(ap + (PACKED ? (size_t)u * sg.qstride : (k < n ? k : 0)));
             }
         }

@@ -69,6 +69,6 @@ def test_noalloc_attention_refuses_sizes_past_the_scratch(hip, torch):
     with pytest.raises(hip.PkHipError):
         hip.attention_noalloc_dev(t, t, t, t, t, t, t, 885, D, H)
     with pytest.raises(hip.PkHipError):
-        hip.attention_noalloc_dev(t, t, t, t, t, t, t, 64, 96, 2)        # heads of 48 dimensions
+        hip.attention_noalloc_dev(t, t, t, t, t, t, t, 64, 80, 2)        # heads of 40 dimensions
     hip.attention_noalloc_dev(t, t, t, t, t, t, t, 0, D, H)              # no frames: nothing to do
     torch.cuda.synchronize()
