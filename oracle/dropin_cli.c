@@ -13,6 +13,12 @@
  * :868-883). FAST 1 is the encoder's fast mode, blocks of 64 inputs
  * (pk_asr_set_fast_mode; blocks of 32 otherwise).
  *
+ * A diarizer's model (pk_model_speakers > 0, core/pktito.h:117-119) is run
+ * through the reference's diarizer instead (core/diar.c's pk_diar_run,
+ * core/pktito.h:660-686: its products go to the same table in blocks of
+ * 32), and every row of speaker probabilities is printed as exact hex
+ * floats, "row i: p0 p1 ...", then "rows N S". FAST is then unused.
+ *
  *   dropin_cli MODEL.pkf SECONDS SEED FAST THREADS --layers OUT
  *
  * also writes the reference's own encoder layers (core/encoder.c:338-368,
@@ -154,6 +160,20 @@ static double unit(void) {
     return (double)((g_s * 0x2545F4914F6CDD1Dull) >> 11) / 9007199254740992.0;
 }
 
+/* pk_diar_fn: a run of rows, printed and counted as they come */
+static long g_rows;
+static int print_rows(void *arg, int64_t row, size_t n, const float *p) {
+    const int S = *(const int *)arg;
+    g_rows += (long)n;
+    for (size_t i = 0; i < n; i++) {
+        printf("row %lld:", (long long)(row + (int64_t)i));
+        for (int s = 0; s < S; s++)
+            printf(" %a", p[i * S + s]);
+        printf("\n");
+    }
+    return 0;
+}
+
 int main(int argc, char **argv) {
     if (argc < 6) {
         fprintf(stderr, "usage: %s MODEL.pkf SECONDS SEED FAST THREADS\n", argv[0]);
@@ -185,6 +205,26 @@ int main(int argc, char **argv) {
         for (int k = 0; k < 4; k++)
             v += 0.12 * env * sin(6.283185307179586 * f[k] * t + ph[k]);
         x[i] = (float)v;
+    }
+    if (pk_model_speakers(m) > 0) {
+        int S = pk_model_speakers(m);
+        pk_diar *d = pk_diar_new(m, threads);
+        if (!d) {
+            fprintf(stderr, "pk_diar_new failed\n");
+            return 1;
+        }
+        if (pk_diar_run(d, x, n, print_rows, &S)) {
+            fprintf(stderr, "pk_diar_run failed\n");
+            return 1;
+        }
+        printf("rows %ld %d\n", g_rows, S);
+        fprintf(stderr, "backend: %s\n", pk_backend());
+        pk_diar_free(d);
+        if (hip)
+            pk_hip_release_model(m);
+        pk_model_free(m);
+        free(x);
+        return 0;
     }
     pk_asr *a = pk_asr_new(m, threads);
     if (!a) {

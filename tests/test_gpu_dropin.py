@@ -10,7 +10,8 @@ dropin_cli, a transcription (core/asr.c's pk_asr_run: the encoder of
 core/encoder.c and the decoder) on whichever table PKTITO_KERNELS names,
 printed token by token. The model is tests/golden/tiny.pkf, the
 reference's tests/data/tiny.pkf (d_model 64, two layers: every product of
-the encoder and the decoder goes through the table).
+the encoder and the decoder goes through the table); for the diarizer,
+tests/golden/tiny-diar.pkf, the reference's tests/data/tiny-diar.pkf.
 
 Bit for bit, as the reference holds every backend (backend/kernels.h:9-14):
 the checkers' verdict lines, and the transcripts compared with cmp's
@@ -129,4 +130,33 @@ def test_transcript_on_the_hip_table_is_refs(seconds, seed, fast):
         assert table in r.stderr.split("backend:")[-1], r.stderr
         outs[table] = r.stdout
     assert outs["hip"].startswith("tokens ") and int(outs["hip"].split()[1]) > 0
+    assert outs["hip"] == outs["ref"]
+
+
+TINY_DIAR = os.path.join(ROOT, "tests", "golden", "tiny-diar.pkf")
+
+
+@pytest.mark.parametrize("seconds,seed", [(20, 1), (40, 2)])
+def test_diarization_on_the_hip_table_is_refs(seconds, seed):
+    """The reference's second caller of the table: its diarizer (core/diar.c,
+    pk_diar_run: the transformer layers' q, k, v, o and feed-forward
+    products, the projection, the upsampling and the head, every one
+    pk_k_gemm_q8 on activations quantized in blocks of 32) on
+    tests/golden/tiny-diar.pkf, the reference's tests/data/tiny-diar.pkf,
+    on 8 threads. Every row of speaker probabilities, as exact hex floats,
+    is the run on ref's; with the diarizer's matrices uploaded at load (the
+    walker's diarizer branch) and released before the free. 40 s cross the
+    model's 27.2 s chunk, so the speaker cache carries between chunks."""
+    cli = program("dropin_cli")
+    outs = {}
+    for table in ("ref", "hip"):
+        say("diarization", table, seconds, seed)
+        env = dict(os.environ, PKTITO_KERNELS=table)
+        r = subprocess.run([cli, TINY_DIAR, str(seconds), str(seed), "0", "8"], capture_output=True, text=True,
+                           env=env, timeout=600)
+        assert r.returncode == 0, (table, r.stderr[-2000:])
+        assert table in r.stderr.split("backend:")[-1], r.stderr
+        outs[table] = r.stdout
+    last = outs["hip"].strip().splitlines()[-1].split()
+    assert last[0] == "rows" and int(last[1]) >= seconds * 25 and int(last[2]) > 0, last
     assert outs["hip"] == outs["ref"]
