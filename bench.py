@@ -777,7 +777,7 @@ def release(layers):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not run "
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not run "
               "(the int8 path would shard frames across GPUs with no exchange)", file=sys.stderr)
         sys.exit(2)
     import torch

@@ -9,8 +9,9 @@
  * The audio is SECONDS of 16 kHz from SEED (xorshift64*: a few tones, their
  * loudness swelling and fading, and noise). Under PKTITO_KERNELS=hip every
  * int8 matrix of the model is uploaded after the load and released before
- * the free: the steps INTEGRATION.md adds to core/model.c (:783-811,
- * :868-883). FAST 1 is the encoder's fast mode, blocks of 64 inputs
+ * the free, as a checkout with the hip backend does in core/model.c's load
+ * and free (:783-811, :868-883: pk_hip_upload_model after the matrices are
+ * bound, pk_hip_release_model before they are unmapped). FAST 1 is the encoder's fast mode, blocks of 64 inputs
  * (pk_asr_set_fast_mode; blocks of 32 otherwise).
  *
  * A diarizer's model (pk_model_speakers > 0, core/pktito.h:117-119) is run

@@ -2,9 +2,10 @@
  * library, as the drop-in tests build it (oracle/Makefile, _ref/dropin_cli).
  *
  * The drop-in's needs are "hip" (libpktito_amd/backend_hip/kernels.c), which
- * a libpktito checkout answers by the one line INTEGRATION.md adds to
- * core/os.c's pk_os_cpu_lacks: the device opens. The reference sources are
- * compiled here unedited, so this build links with --wrap=pk_os_cpu_lacks
+ * a libpktito checkout with the hip backend answers by one more line in
+ * core/os.c's pk_os_cpu_lacks: "hip" is met when pk_hip_init() opens the
+ * device. The reference sources are
+ * compiled here unedited, so the harness links with --wrap=pk_os_cpu_lacks
  * and answers it in this wrapper instead, every other need going to the
  * reference's own function (core/os.c:905-911). */
 #include "pk_hip.h"

@@ -14,7 +14,7 @@ the encoder and the decoder goes through the table); for the diarizer,
 tests/golden/tiny-diar.pkf, the reference's tests/data/tiny-diar.pkf.
 
 Bit for bit, as the reference holds every backend (backend/kernels.h:9-14):
-the checkers' verdict lines, and the transcripts compared with cmp's
+kcheck's and q8check's verdict lines, and the transcripts compared with cmp's
 strictness as tests/check-c.sh:73-81 does."""
 import os
 import re
@@ -80,7 +80,7 @@ def test_kcheck_holds_the_hip_table_to_ref():
     """tests/kcheck.c without a model: the quantizer's cases (non-finite
     blocks, the 2^-121 edge, xs > n, blocks of 32 and 64 and whole columns)
     and gemm_q8's (random shapes, qb, bias, add, pitches, interior panels,
-    the x86 backends' tile edges), each a buffer of the checker's own (the
+    the x86 backends' tile edges), each a buffer of kcheck's own (the
     table copies and repacks weights it was not given at upload), plus the
     float kernels the table takes from the CPU."""
     say("kcheck")
