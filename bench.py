@@ -77,6 +77,8 @@ def parse():
                    help="only M-row products through rotated K x N matrices, 50 launches (for rocprofv3)")
     p.add_argument("--profile-decoder", action="store_true",
                    help="the decoder's token steps only (graphs of a prediction and a joint, no CPU leg)")
+    p.add_argument("--profile-step", action="store_true",
+                   help="only the per-row layer step at one minute of audio, its graph replayed --steps times")
     p.add_argument("--peaks", action="store_true",
                    help="only the on-machine check of the int8 MFMA and HBM read peaks")
     p.add_argument("--copy-calibration", action="store_true",
@@ -794,6 +796,12 @@ def main():
         return
     if args.profile_decoder:
         print(json.dumps({"profiled": "decoder_steps", **decoder_steps(pk, torch, False)}))
+        return
+    if args.profile_step:
+        prods = make_layer(pk, torch, M, seed=1)
+        graph = graph_of(torch, layer_step(pk, prods))
+        ms = time_graph(torch, graph, args.steps, args.warmup)
+        print(json.dumps({"profiled": "layer_step", "M": M, "replays": args.steps, "ms_per_step": round(ms, 5)}))
         return
     if args.profile_layer:
         us, _ = device_layer(pk, torch, M, args.profile_layer, reps=args.steps, warmup=args.warmup)
