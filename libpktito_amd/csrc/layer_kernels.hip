@@ -567,22 +567,32 @@ __global__ __launch_bounds__(256) void att_dims_kernel(float *__restrict__ S, ui
         }
     };
     /* ns is even (dk a multiple of 64): stages in pairs, the buffers and
-     * register sets alternating statically */
+     * register sets alternating statically. No load is issued for a stage
+     * past the last: one still in flight at the end would hold every
+     * output store behind a wait for it (its registers are reused), which
+     * cost a workgroup ~5 us of its ~14. */
     Regs g0, g1;
     load(g0, 0);
     load(g1, kSD);
     store(g0, 0);
     __syncthreads();
     for (uint32_t st = 0; st < ns; st += 2) {
-        load(g0, (st + 2) * kSD);
+        const bool more = st + 2 < ns;
+        if (more)
+            load(g0, (st + 2) * kSD);
         mult(0);
         store(g1, 1);
         __syncthreads();
-        load(g1, (st + 3) * kSD);
+        if (more)
+            load(g1, (st + 3) * kSD);
         mult(1);
-        store(g0, 0);
+        if (more)
+            store(g0, 0);
         __syncthreads();
     }
+    /* nothing is in flight here; saying so spares the stores below a wait
+     * each for loads the compiler cannot rule out */
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));      /* vmcnt(0) */
     if (!BAND) {
 #pragma unroll
         for (int r = 0; r < 32; r++) {
@@ -593,27 +603,28 @@ __global__ __launch_bounds__(256) void att_dims_kernel(float *__restrict__ S, ui
                 S[((size_t)h * T + qi) * Ts + (uint32_t)kj] = acc[r];
         }
     } else {
-        /* a block's 16 old scores first, then their sums: the loads need
-         * not wait on the stores (no two registers hold the same (i, j));
-         * offsets from the head's scores fit 32 bits (the launcher checks) */
+        /* all 32 old scores first, one wait, then their sums: no store
+         * waits on another (no two registers hold the same (i, j); a load
+         * issued after a store would wait for it, the counter being in
+         * order); offsets from the head's scores fit 32 bits (the launcher
+         * checks) */
         float *Sh = S + (size_t)h * T * Ts;
+        uint32_t at[32];
+        float old[32];
 #pragma unroll
-        for (int blk = 0; blk < 2; blk++) {
-            uint32_t at[16];
-            float old[16];
-#pragma unroll
-            for (int rr = 0; rr < 16; rr++) {
-                const uint32_t qi = i0 + 32 * wq + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
-                const int64_t kj = y0 + 64 * wy + 32 * blk + (lane & 31) - ((int64_t)T - 1 - (int64_t)qi);
-                const bool in = qi < T && kj >= 0 && kj < (int64_t)T;
-                at[rr] = in ? qi * Ts + (uint32_t)kj : ~0u;
-                old[rr] = in ? Sh[at[rr]] : 0.0f;
-            }
-#pragma unroll
-            for (int rr = 0; rr < 16; rr++)
-                if (at[rr] != ~0u)
-                    Sh[at[rr]] = old[rr] + acc[16 * blk + rr];
+        for (int r = 0; r < 32; r++) {
+            const int blk = r >> 4, rr = r & 15;
+            const uint32_t qi = i0 + 32 * wq + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+            const int64_t kj = y0 + 64 * wy + 32 * blk + (lane & 31) - ((int64_t)T - 1 - (int64_t)qi);
+            const bool in = qi < T && kj >= 0 && kj < (int64_t)T;
+            at[r] = in ? qi * Ts + (uint32_t)kj : ~0u;
+            old[r] = in ? Sh[at[r]] : 0.0f;
         }
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));      /* vmcnt(0) */
+#pragma unroll
+        for (int r = 0; r < 32; r++)
+            if (at[r] != ~0u)
+                Sh[at[r]] = old[r] + acc[r];
     }
 }
 
