@@ -30,7 +30,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libpkhip.so")
 SOURCES = [os.path.join(HERE, "csrc", n)
-           for n in ("q8_kernels.hip", "layer_kernels.hip", "dec_kernels.hip", "diag_kernels.hip", "pk_hip.cpp")]
+           for n in ("q8_kernels.hip", "q8_stream.hip", "layer_kernels.hip", "dec_kernels.hip", "diag_kernels.hip", "pk_hip.cpp")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

@@ -181,6 +181,18 @@ struct JobTable {
 
 int launch_gemm_batch(const JobTable &jobs, hipStream_t s, const char **name);
 
+/* The streamed product's tilings (q8_stream.hip): persistent workgroups over
+ * the tile list, loader waves apart from the MFMA waves; per-row blocks, one
+ * segment or a batch of jobs sharing ku. */
+struct StreamCfg {
+    const char *name;
+    uint32_t bn, bm, ups, slots;        /* channels x frames, units a stage, ring slots */
+    void (*run)(const GemmArgs &, const SegTable &, hipStream_t);
+    void (*batch)(const JobTable &, hipStream_t);
+};
+const StreamCfg *stream_cfg(int i);     /* nullptr past the last */
+int stream_count();
+
 }  // namespace pkq8
 
 #endif

@@ -1718,15 +1718,19 @@ constexpr int kNRing = sizeof kRing / sizeof kRing[0];
 /* A forced tiling for tests and tuning (set_ring), -1 for the heuristic. */
 static int g_forced_ring = -1;
 
+/* Tiling indexes: [0, kNRing) the per-launch tiles above, then
+ * [kNRing, kNRing + stream_count()) the streamed product's (q8_stream.hip). */
 int set_ring(int i) {
     const int was = g_forced_ring;
-    g_forced_ring = i >= 0 && i < kNRing ? i : -1;
+    g_forced_ring = i >= 0 && i < kNRing + stream_count() ? i : -1;
     return was;
 }
 
-int ring_count() { return kNRing; }
+int ring_count() { return kNRing + stream_count(); }
 
-const char *ring_name(int i) { return i >= 0 && i < kNRing ? kRing[i].name : ""; }
+const char *ring_name(int i) {
+    return i >= 0 && i < kNRing ? kRing[i].name : i >= kNRing && i < kNRing + stream_count() ? stream_cfg(i - kNRing)->name : "";
+}
 
 /* whether tiling i takes ku units a panel: ring_tile runs whole passes of
  * four stages; pipe_tile needs its slots' worth of stages to start, and its
@@ -1734,6 +1738,8 @@ const char *ring_name(int i) { return i >= 0 && i < kNRing ? kRing[i].name : "";
  * a stage the stages past the slots' first fill must be even in number (a
  * pass past them would load a stage beyond the last) */
 static bool fits(int i, uint32_t ku) {
+    if (i < 0 || i >= kNRing)
+        return false;
     const RingCfg &c = kRing[i];
     if (c.slots == 0)
         return ku % (4 * c.ups) == 0;
@@ -1791,6 +1797,45 @@ static int pick_blocked(uint32_t rows, uint64_t frames, uint32_t ku) {
     if (g_forced_ring < 0 && c == 13 && w8 >= 0 && fits(w8, ku))
         return w8;
     return c;
+}
+
+/* whether streamed tiling i (an index of kStream) takes ku units a panel: a
+ * tile's stages fill the ring, and its sub-steps are whole passes */
+static bool stream_fits(int i, uint32_t ku) {
+    const StreamCfg &c = *stream_cfg(i);
+    const uint32_t spi = c.ups > 2 ? c.ups : 2;
+    return ku % spi == 0 && ku / c.ups >= c.slots;
+}
+
+/* whether a call's weights and activations span less than 2 GiB from their
+ * first bytes: the streamed product reads them through buffer resources with
+ * 32-bit offsets */
+static bool stream_spans_fit(const GemmArgs &g, const Seg &sg) {
+    constexpr uint64_t lim = (uint64_t)1 << 31;
+    const uint64_t wspan = (uint64_t)g.ku * g.wstride;
+    const uint64_t aspan = sg.qstride ? (uint64_t)g.ku * sg.qstride : (uint64_t)sg.T * g.n;
+    return wspan < lim && aspan < lim;
+}
+
+/* The streamed tiling (an index of stream_cfg) for a per-row product of one
+ * segment, or -1 for the per-launch tiles: the forced one where it fits;
+ * else 256 x 128 streamed tiles where there are at least 400 of them, or 200
+ * with deep inputs (4096). Measured at 7500 frames (each product alone): ff
+ * up 41-44 against 46-47 us, pw1 24.2 against 25.9, the positions' 14999
+ * rows 26-30 against 28-34, ff down 32.7-34.3 against 34.2-36.1; the 236-tile
+ * products with 1024 inputs (q, k, v, o, pw2) and the attention's batch run
+ * faster on the per-launch tiles (two workgroups a CU fill each other's
+ * barrier waits where one tile a CU leaves nothing to stream). */
+static int pick_stream(uint32_t rows, uint64_t frames, uint32_t ku, bool batch = false) {
+    if (g_forced_ring >= kNRing) {
+        const int i = g_forced_ring - kNRing;
+        return stream_fits(i, ku) ? i : -1;
+    }
+    if (g_forced_ring >= 0 || batch || !stream_fits(0, ku))
+        return -1;
+    const StreamCfg &c = *stream_cfg(0);
+    const uint64_t tiles = (uint64_t)((rows + c.bn - 1) / c.bn) * ((frames + c.bm - 1) / c.bm);
+    return tiles >= 400 || (ku >= 64 && tiles >= 200) ? 0 : -1;
 }
 
 template <int WN, int WM, int TN, int TM, int MODE>
@@ -1855,6 +1900,14 @@ int launch_gemm(const GemmArgs &ga, const SegTable &tab, hipStream_t s, const ch
         }
         return hipPeekAtLastError() == hipSuccess ? 0 : -1;
     }
+    if (mode == 0 && tab.nseg == 1 && stream_spans_fit(g, tab.s[0])) {
+        const int c = pick_stream(g.rows, frames, g.ku);
+        if (c >= 0) {
+            stream_cfg(c)->run(g, tab, s);
+            *name = stream_cfg(c)->name;
+            return hipPeekAtLastError() == hipSuccess ? 0 : -1;
+        }
+    }
     if (mode == 0) {
         const int c = pick_ring(g.rows, frames, g.ku);
         kRing[c].run(g, tab, s);
@@ -1914,6 +1967,17 @@ int launch_gemm_batch(const JobTable &jobs_in, hipStream_t s, const char **name)
      * job shares the blocks (the caller checks) */
     const GemmArgs &g0 = jobs.g[0];
     const int mode = g0.qb == g0.n ? 0 : g0.qb == 64 ? 1 : g0.qb == 32 ? 2 : -1;
+    bool spans = true;
+    for (uint32_t j = 0; j < jobs.njobs; j++)
+        spans = spans && stream_spans_fit(jobs.g[j], jobs.s[j]);
+    if (mode == 0 && spans) {
+        const int sc = pick_stream(rows, frames, g0.ku, true);
+        if (sc >= 0) {
+            stream_cfg(sc)->batch(jobs, s);
+            *name = stream_cfg(sc)->name;
+            return hipPeekAtLastError() == hipSuccess ? 0 : -1;
+        }
+    }
     const int c = mode == 0 ? pick_ring(rows, frames, g0.ku) : pick_blocked(rows, frames, g0.ku);
     auto batch = mode == 0 ? kRing[c].batch : mode == 1 ? kRing[c].batch64 : mode == 2 ? kRing[c].batch32 : nullptr;
     if (batch) {

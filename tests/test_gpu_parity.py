@@ -368,7 +368,7 @@ def test_every_tiling(hip):
                         hip.gemm_q8(out, os_, w, ws[r0:], bias[r0:], rows, hip.make_act(q, d, K, K, M), add,
                                     w_offset=r0 * K, out_offset=r0)
                         if M > 16:
-                            assert hip.last_kernel().startswith(("ring", "pipe")), hip.last_kernel()
+                            assert hip.last_kernel().startswith(("ring", "pipe", "stream")), hip.last_kernel()
                     assert same(out, want), (ti, M, K, N, add)
     finally:
         hip.force_tiling(-1)

@@ -68,3 +68,32 @@ def test_product_kernels_wait_before_touching_lds_reads(kernels_asm):
     assert any("ring" in n for n in fns) and any("pipe" in n for n in fns), sorted(fns)
     bad = {name: v[:2] for name, v in ((n, lds_waits.violations(b)) for n, b in fns.items()) if v}
     assert not bad, bad
+
+
+@pytest.fixture(scope="module")
+def stream_asm(tmp_path_factory):
+    from libpktito_amd import build
+    return _asm(tmp_path_factory, next(s for s in build.SOURCES if s.endswith("q8_stream.hip")))
+
+
+def test_streamed_kernels_wait_before_touching_lds_reads(stream_asm):
+    fns = lds_waits.functions(stream_asm, r"gemm_stream_kernel")
+    assert fns, "no streamed kernel in the assembly"
+    bad = {name: v[:2] for name, v in ((n, lds_waits.violations(b)) for n, b in fns.items()) if v}
+    assert not bad, bad
+
+
+def test_streamed_kernels_mfma_loop_never_waits_on_vmcnt(stream_asm):
+    """The streamed kernels' MFMA waves issue no global loads in their K loop,
+    and their stores drain under the next tile's loop only if nothing there
+    waits on vmcnt (which counts stores too): no basic block that holds an
+    MFMA may hold a vmcnt wait (a residual load left in flight across a tile,
+    or a spill, would put one there)."""
+    fns = lds_waits.functions(stream_asm, r"gemm_stream_kernel")
+    for name, body in fns.items():
+        blocks, _ = lds_waits._blocks(body)
+        mfma = [b for b in blocks if any(t.startswith("v_mfma") for t in b)]
+        assert mfma, name
+        waits = [t for b in mfma for t in b if t.startswith("s_waitcnt") and "vmcnt" in t]
+        assert not waits, (name, waits[:3])
+        assert "scratch_" not in "\n".join(body), name
