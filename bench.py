@@ -767,6 +767,12 @@ def roofline_of(dom, dname, dkms):
              kernel_us=round(dkms * 1e3, 3), bytes_per_launch=dbytes, ops_per_launch=dom.ops(),
              traffic=recorded_traffic(dname, dom.M, dom.K, dom.N))
     r["frac"] = round(r["achieved"] / r["peak"], 4)
+    # achieved and frac count the algorithmic (minimum) bytes a launch; the
+    # same launch's profiled HBM traffic, where a summary covers it, gives
+    # the rate the memory actually moved, named apart
+    if bound == "hbm" and r["traffic"]:
+        r["achieved_traffic"] = round(r["traffic"] / (dkms * 1e-3) / 1e9, 1)
+        r["frac_traffic"] = round(r["achieved_traffic"] / r["peak"], 4)
     return r
 
 

@@ -238,7 +238,8 @@ int pk_hip_layernorm_dev(float *x, uint32_t T, uint32_t n, const float *w, const
 
 /* The attention's float part (core/encoder.c:280-327): H heads of D / H
  * dimensions (a multiple of 16; heads of a multiple of 64 run on the
- * tiled kernels, others on one thread an output), o [T][D] from the
+ * tiled kernels, others on one thread an output: fine for the tiny models'
+ * 16-wide heads, slow, with no tiling, for long inputs), o [T][D] from the
  * products' outputs q, k,
  * v [T][D] and the positions' p [2T - 1][D] with the biases u and v [D]:
  * Transformer-XL's scores, the softmax, the weighted values, each output
@@ -255,8 +256,13 @@ int pk_hip_attention_dev(float *o, const float *q, const float *k, const float *
  * callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
  * pk_hip_attention_workspace(T, H) must be at most 24 MiB (T up to 884 at 8
- * heads), else PK_HIP_EINVAL. Every call on one GPU shares the array:
- * calls that overlap on one GPU (on two streams, or two threads) race. */
+ * heads), else PK_HIP_EINVAL. Every call on one GPU shares the array; it
+ * keeps the last call's contents, and each call rewrites every score it
+ * reads. Outside stream capture a call's kernels wait for the previous
+ * call's on that GPU (an event the library records after each call), so
+ * calls on two streams or threads take turns. Under capture the call adds
+ * no such wait: the caller orders a graph's replays against each other and
+ * against other calls (replays of one graph on one stream are ordered). */
 int pk_hip_attention_noalloc_dev(float *o, const float *q, const float *k, const float *v, const float *p,
                                  const float *bias_u, const float *bias_v, uint32_t T, uint32_t D, uint32_t H,
                                  void *stream);

@@ -924,7 +924,11 @@ int launch_norm(float *x, uint32_t n, uint32_t T, const float *w, const float *b
  * content chain fma(k, q + u) and the position chain fma(p_m, q + v) over
  * the head's dimensions in order from +0, m = T - 1 - i + j, then their sum;
  * an output is the chain fma(v_j, e_ij * (1 / sum_i)) over the T keys in
- * order from +0. */
+ * order from +0. Made for narrow heads at short lengths (the tiny models'
+ * 16-wide heads): each thread walks its chains serially from global memory,
+ * so the time grows as T^2 * D with no tiling at all; at thousands of frames
+ * with 80- or 96-wide heads this is many times the tiled kernels' time for
+ * 64-wide heads of the same model size. */
 __global__ __launch_bounds__(256) void att_scores_small_kernel(float *__restrict__ S, uint32_t Ts,
                                                                const float *__restrict__ qf,
                                                                const float *__restrict__ kf,
@@ -989,8 +993,9 @@ static __device__ __align__(256) char scratch[kStaticScratchBytes];
 
 static std::mutex g_scratch_mu;
 static void *g_scratch_at[kMaxDevices];
+static hipEvent_t g_scratch_ev[kMaxDevices];
 
-void *static_scratch(int dev, int *err) {
+void *static_scratch(int dev, int *err, hipEvent_t *last) {
     if (dev < 0 || dev >= kMaxDevices) {
         *err = (int)hipErrorInvalidDevice;
         return nullptr;
@@ -1004,13 +1009,23 @@ void *static_scratch(int dev, int *err) {
         void *p = nullptr;
         if (e == hipSuccess)
             e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        hipEvent_t ev = nullptr;
+        if (e == hipSuccess && p)
+            e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
         if (e != hipSuccess || !p) {
+            /* HIP keeps a failed call's error until it is read: read it
+             * here, so that the next launch of any entry on this thread
+             * does not report it as its own */
+            (void)hipGetLastError();
             *err = (int)(e != hipSuccess ? e : hipErrorInvalidSymbol);
             return nullptr;
         }
         g_scratch_at[dev] = p;
+        g_scratch_ev[dev] = ev;
     }
     *err = 0;
+    if (last)
+        *last = g_scratch_ev[dev];
     return g_scratch_at[dev];
 }
 

@@ -101,8 +101,9 @@ void init_once() {
     }
     g_dev = dev;
     g_init = PK_HIP_OK;
-    /* the static scratch's address on this device, taken once now (a
-     * failure here fails only the entry that uses it) */
+    /* the static scratch's address and event on this device, taken once
+     * now (a failure here, its HIP error read and cleared, fails only the
+     * entry that uses them) */
     int se = 0;
     (void)pkq8::static_scratch(dev, &se);
 }
@@ -1042,11 +1043,27 @@ int pk_hip_attention_noalloc_dev(float *o, const float *q, const float *k, const
     int dev = -1;
     PK_TRY(hipGetDevice(&dev));
     int se = 0;
-    void *ws = pkq8::static_scratch(dev, &se);
+    hipEvent_t last = nullptr;
+    void *ws = pkq8::static_scratch(dev, &se, &last);
     if (!ws)
         return hip_fail((hipError_t)se, "attention_noalloc_dev: the static scratch's address");
+    /* Calls on one GPU share the scratch: outside stream capture each call
+     * waits on its stream for the last one to finish with it (an event of
+     * the device, recorded after every call; the lock keeps wait, launch and
+     * record of two host threads from interleaving). A captured call records
+     * neither (a captured wait on an event recorded outside the capture is
+     * not allowed): the graph's own order, and the caller's between replays
+     * and other calls, keep its uses apart. */
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    PK_TRY(hipStreamIsCapturing((hipStream_t)stream, &cs));
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lk(mu);
+    if (cs == hipStreamCaptureStatusNone)
+        PK_TRY(hipStreamWaitEvent((hipStream_t)stream, last, 0));
     PK_LAUNCH(pkq8::launch_attention(o, (float *)ws, q, k, v, p, bias_u, bias_v, T, D, H, (hipStream_t)stream),
               "attention launch");
+    if (cs == hipStreamCaptureStatusNone)
+        PK_TRY(hipEventRecord(last, (hipStream_t)stream));
     g_kernel = "attention";
     return PK_HIP_OK;
 }

@@ -133,10 +133,12 @@ int launch_attention(float *of, float *ws, const float *qf, const float *kf, con
 /* The attention's static scratch (layer_kernels.hip) for callers that
  * cannot allocate: its bytes, and its address on device dev, which must be
  * current (taken once a device; NULL with the HIP error in *err if it
- * cannot be had). */
+ * cannot be had), with, in *last when last is set, an event of that device
+ * created at the same time, which the entry records after each use so that
+ * the next use waits for it. */
 constexpr size_t kStaticScratchBytes = (size_t)24 << 20;
 constexpr int kMaxDevices = 64;
-void *static_scratch(int dev, int *err);
+void *static_scratch(int dev, int *err, hipEvent_t *last = nullptr);
 
 int launch_dwq(int8_t *qp, float *d, const float *u, uint32_t T, uint32_t D, const float *w, const float *b,
                uint32_t K, uint32_t qb, hipStream_t s);

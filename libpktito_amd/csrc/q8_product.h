@@ -1,5 +1,6 @@
 /* Device helpers of the int8 products shared by their kernel files
- * (q8_kernels.hip and the layer's kernels): non-temporal output stores, LDS DMA
+ * (q8_kernels.hip, the per-launch tiles; q8_stream.hip, the streamed tiles;
+ * tests/test_lds_waits.py checks both files' assembly): non-temporal output stores, LDS DMA
  * address spaces, explicit vmcnt / lgkmcnt waits, LDS fragment reads issued
  * as inline asm, compile-time unrolling, and the XCD-aware tile order. */
 #ifndef PK_Q8_PRODUCT_H

@@ -254,11 +254,12 @@ def test_layer_model_shapes(hip, torch, T, qb):
     run_layer(hip, torch, 1024, 8, 4096, 9, T, qb, seed=T + qb)
 
 
-@pytest.mark.parametrize("T,qb", [(750, 32)])
+@pytest.mark.parametrize("T,qb", [(750, 32), (750, 64)])
 def test_layer_model_shapes_at_a_minute(hip, torch, T, qb):
     """The whole layer at the bench's size: a minute of audio (750 frames),
-    d_model 1024, 8 heads, ff 4096, 9 taps, blocks of 32: the band of
-    position rows and the 750-key softmax and PV the bench times."""
+    d_model 1024, 8 heads, ff 4096, 9 taps, blocks of 32 (the encoder's
+    default) and of 64 (its fast mode): the band of position rows and the
+    750-key softmax and PV the bench times."""
     run_layer(hip, torch, 1024, 8, 4096, 9, T, qb, seed=T + qb)
 
 
@@ -284,3 +285,18 @@ def test_layer_attention_output_special_values(hip, torch, valu, qb):
         run_layer(hip, torch, 256, 4, 512, 9, 37, qb, seed=91 + qb, tweak=plant)
     finally:
         hip.force_attention(was)
+
+
+@pytest.mark.parametrize("qb", [32, 64])
+def test_layer_narrow_heads_special_values(hip, torch, qb):
+    """The same planted special values through heads 16 wide (d_model 64, 4
+    heads), which take the attention's one-thread-an-output kernels: head 0's
+    channel 5 NaN, head 1's channel 20 infinite, head 2 zero and head 3
+    subnormal; bit for bit against the oracle."""
+    def plant(w):
+        s = w["v_s"]
+        s[5] = np.float32(np.nan)
+        s[20] = np.float32(np.inf)
+        s[32:48] = 0.0
+        s[48:64] = np.float32(1e-44)
+    run_layer(hip, torch, 64, 4, 128, 9, 37, qb, seed=17 + qb, tweak=plant)

@@ -72,3 +72,46 @@ def test_noalloc_attention_refuses_sizes_past_the_scratch(hip, torch):
         hip.attention_noalloc_dev(t, t, t, t, t, t, t, 64, 80, 2)        # heads of 40 dimensions
     hip.attention_noalloc_dev(t, t, t, t, t, t, t, 0, D, H)              # no frames: nothing to do
     torch.cuda.synchronize()
+
+
+def test_noalloc_attention_under_graph_capture(hip, torch):
+    """The entry captured into a HIP graph (what it exists for), replayed
+    several times with eager work of the library between replays and new
+    inputs copied in before each: every replay's output is
+    pk_hip_attention_dev's on the same inputs, bit for bit."""
+    T, D, H = 300, 512, 8
+    ops = operands(torch, T, D, 77)
+    ws = torch.empty((hip.attention_workspace(T, H),), dtype=torch.uint8, device="cuda")
+    got = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    say("attention captured", T, D, H)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        hip.attention_noalloc_dev(got, *ops, T, D, H)     # once outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        hip.attention_noalloc_dev(got, *ops, T, D, H)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        fresh = operands(torch, T, D, 1000 + rep)
+        for dst, src in zip(ops, fresh):
+            dst.copy_(src)
+        want = torch.full((T, D), 5.0, dtype=torch.float32, device="cuda")
+        say("eager attention between replays", rep)
+        hip.attention_dev(want, *ops, T, D, H, ws)
+        # an eager call of the entry itself on other frames, so the scratch
+        # holds other scores when the replay starts
+        other = operands(torch, 64, D, 2000 + rep)
+        junk = torch.empty((64, D), dtype=torch.float32, device="cuda")
+        hip.attention_noalloc_dev(junk, *other, 64, D, H)
+        torch.cuda.synchronize()
+        got.fill_(7.0)
+        torch.cuda.synchronize()
+        say("replay", rep)
+        g.replay()
+        torch.cuda.synchronize()
+        w = want.cpu().numpy()
+        assert np.isfinite(w).all()
+        assert np.array_equal(bits(got.cpu().numpy()), bits(w)), rep
