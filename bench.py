@@ -349,12 +349,15 @@ def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20, rows=(1, 4, 16), lau
             d = torch.empty((M,), dtype=torch.float32, device=dev)
             pk.quantize_dev(q, d, x, K, K, M, K)
             o = torch.empty((M, N), dtype=torch.float32, device=dev)
+            # the split over K's workspace, zero, shared by the rotation's
+            # launches (one stream: they run one after another)
+            work = torch.zeros((pk.gemm_workspace(N),), dtype=torch.uint8, device=dev)
 
             if launches:
                 # eager launches over the rotation, for a counter run
                 for i in range(launches):
                     m = mats[i % len(mats)]
-                    pk.gemm_q8_dev(o, N, m, 0, N, None, None, q, d, K, K, M, 0, ws_ptr=m.dev_scales)
+                    pk.gemm_q8_dev(o, N, m, 0, N, None, None, q, d, K, K, M, 0, ws_ptr=m.dev_scales, work=work)
                 torch.cuda.synchronize()
                 out.append(dict(M=M, K=K, N=N, launches=launches, kernel=pk.last_kernel(),
                                 bytes_per_launch=N * K + 4 * N + M * K + 4 * M + 4 * M * N))
@@ -362,7 +365,7 @@ def skinny_rates(pk, torch, shapes, budget_bytes=640 << 20, rows=(1, 4, 16), lau
 
             def fn():
                 for m in mats:
-                    pk.gemm_q8_dev(o, N, m, 0, N, None, None, q, d, K, K, M, 0, ws_ptr=m.dev_scales)
+                    pk.gemm_q8_dev(o, N, m, 0, N, None, None, q, d, K, K, M, 0, ws_ptr=m.dev_scales, work=work)
             gr = graph_of(torch, fn)
             ms = min(time_graph(torch, gr, 2, 1) for _ in range(3)) / len(mats)
             kname = pk.last_kernel()

@@ -166,6 +166,35 @@ int pk_hip_gemm_q8_packed_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_
                               const float *ws, const float *bias, const pk_hip_act *a, const int8_t *qp,
                               int add, int rmode, void *stream);
 
+/* The few-frame products (T <= 16, blocks of the whole row: the decoder's
+ * per-row callers, core/decoder.c:53-63 and :83-101, and the skinny
+ * configs) bound by streaming the weights once: with a workspace, the K
+ * inputs of each 16-row panel are split over up to 8 workgroups, so a
+ * matrix of few panels (1024 or 1040 rows: 64 or 65 panels) spreads its
+ * weights over the chip's CUs instead of one CU a panel. The workgroups of
+ * a panel hand their exact int32 sums over in the workspace and the last
+ * one runs the epilogue once: the same bits as the entries above. No
+ * counterpart in the reference (its CPU calls have no split to make).
+ *
+ * pk_hip_gemm_workspace(rows): the bytes of workspace a product of rows
+ * channels takes. The workspace is device memory, 256-byte aligned and zero
+ * before its first use: it starts with a counter a panel, which every call
+ * leaves at zero again, then the partial sums, which a call writes before it
+ * reads them. Calls that overlap in time (two streams) need workspaces of
+ * their own. */
+size_t pk_hip_gemm_workspace(uint32_t rows);
+
+/* pk_hip_gemm_q8_dev and pk_hip_gemm_q8_packed_dev with that workspace
+ * (work, work_bytes >= pk_hip_gemm_workspace(rows)); NULL: no split. Other
+ * calls (T > 16, blocks of 32 or 64) run as the entries above and leave it
+ * untouched. */
+int pk_hip_gemm_q8_ws_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
+                          const float *ws, const float *bias, const pk_hip_act *a, int add, int rmode,
+                          void *work, size_t work_bytes, void *stream);
+int pk_hip_gemm_q8_packed_ws_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
+                                 const float *ws, const float *bias, const pk_hip_act *a, const int8_t *qp,
+                                 int add, int rmode, void *work, size_t work_bytes, void *stream);
+
 /* One segment of a grouped product: its own activations and outputs. */
 typedef struct {
     float      *out;
@@ -356,6 +385,12 @@ const char *pk_hip_last_kernel(void);
 int pk_hip_tilings(void);
 const char *pk_hip_tiling_name(int index);
 int pk_hip_force_tiling(int index);
+
+/* Tests and tuning: how many workgroups share a panel in every later split
+ * few-frame product (1..8; fewer where the panel has fewer units), -1 the
+ * automatic choice; returns the one forced before. All compute the same
+ * bits. */
+int pk_hip_force_split(int splits);
 
 /* Tests and tuning: forcing the packed quantize's kernel for every later
  * launch in the process: 0 one wave a column (or a wave a 1024-input chunk

@@ -82,6 +82,8 @@ _SIGS = {
     "pk_hip_last_kernel": (ctypes.c_char_p, []),
     "pk_hip_tilings": (ctypes.c_int, []),
     "pk_hip_force_tiling": (ctypes.c_int, [ctypes.c_int]),
+    "pk_hip_force_split": (ctypes.c_int, [ctypes.c_int]),
+    "pk_hip_gemm_workspace": (ctypes.c_size_t, [ctypes.c_uint32]),
     "pk_hip_tiling_name": (ctypes.c_char_p, [ctypes.c_int]),
     "pk_hip_force_quantize": (ctypes.c_int, [ctypes.c_int]),
     "pk_hip_force_attention": (ctypes.c_int, [ctypes.c_int]),
@@ -107,6 +109,15 @@ _SIGS = {
                                                  ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
                                                  ctypes.POINTER(Act), ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                                  ctypes.c_void_p]),
+    "pk_hip_gemm_q8_ws_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_uint32,
+                                             ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(Act),
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+                                             ctypes.c_void_p]),
+    "pk_hip_gemm_q8_packed_ws_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                                    ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
+                                                    ctypes.c_void_p, ctypes.POINTER(Act), ctypes.c_void_p,
+                                                    ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+                                                    ctypes.c_void_p]),
     "pk_hip_gemm_q8_grouped_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                   ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(Seg),
                                                   ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]),
@@ -297,15 +308,33 @@ def quantize_dev(q, d, x, n, qb, T, xs, stream=None):
 
 
 def gemm_q8_dev(out, os_, m, r0, rows, ws, bias, q, d, n, qb, T, add, rmode=0, stream=None,
-                ws_ptr=None, out_ptr=None):
+                ws_ptr=None, out_ptr=None, work=None):
     """gemm_q8 on device tensors against an uploaded Q8Matrix m, rows
     [r0, r0 + rows). ws (or ws_ptr) and bias start at row r0; out (or
-    out_ptr) at the first output."""
+    out_ptr) at the first output. With work (a zeroed uint8 tensor of
+    gemm_workspace(rows) bytes), few-frame products split K over the
+    workspace (pk_hip_gemm_q8_ws_dev)."""
     a = Act(_dptr(q), _dptr(d), n, qb, T)
     wsp = ws_ptr if ws_ptr is not None else _dptr(ws)
     op = out_ptr if out_ptr is not None else _dptr(out)
+    if work is not None:
+        _check(lib().pk_hip_gemm_q8_ws_dev(op, os_, m.handle, r0, rows, wsp, _dptr(bias), ctypes.byref(a),
+                                           int(add), rmode, _dptr(work), work.numel(), _stream(stream)))
+        return
     _check(lib().pk_hip_gemm_q8_dev(op, os_, m.handle, r0, rows, wsp, _dptr(bias),
                                     ctypes.byref(a), int(add), rmode, _stream(stream)))
+
+
+def gemm_workspace(rows):
+    """Bytes of workspace a split few-frame product of rows channels takes
+    (pk_hip_gemm_workspace)."""
+    return lib().pk_hip_gemm_workspace(rows)
+
+
+def force_split(splits):
+    """Force how many workgroups share a panel in split few-frame products
+    (1..8, -1 automatic); returns the one forced before."""
+    return lib().pk_hip_force_split(splits)
 
 
 def packed_bytes(n, T):
@@ -322,11 +351,17 @@ def quantize_packed_dev(q, qp, d, x, n, T, xs, stream=None, qb=None):
 
 
 def gemm_q8_packed_dev(out, os_, m, r0, rows, ws_ptr, bias, qp, d, n, T, add, rmode=0, stream=None, out_ptr=None,
-                       qb=None):
+                       qb=None, work=None):
     """gemm_q8 on device tensors with the activations from the packed copy qp
-    (blocks of qb inputs: the whole row by default, or 32 or 64)."""
+    (blocks of qb inputs: the whole row by default, or 32 or 64); work as for
+    gemm_q8_dev (pk_hip_gemm_q8_packed_ws_dev)."""
     a = Act(None, _dptr(d), n, qb or n, T)
     op = out_ptr if out_ptr is not None else _dptr(out)
+    if work is not None:
+        _check(lib().pk_hip_gemm_q8_packed_ws_dev(op, os_, m.handle, r0, rows, ws_ptr, _dptr(bias),
+                                                  ctypes.byref(a), _dptr(qp), int(add), rmode, _dptr(work),
+                                                  work.numel(), _stream(stream)))
+        return
     _check(lib().pk_hip_gemm_q8_packed_dev(op, os_, m.handle, r0, rows, ws_ptr, _dptr(bias), ctypes.byref(a),
                                            _dptr(qp), int(add), rmode, _stream(stream)))
 

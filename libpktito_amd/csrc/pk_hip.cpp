@@ -155,6 +155,8 @@ struct Ctx {
     hipStream_t stream = nullptr;
     char *dev = nullptr;
     size_t cap = 0;
+    char *skw = nullptr;                    /* the split few-frame products' workspace, zeroed */
+    size_t skw_cap = 0;
     char *host[2] = { nullptr, nullptr };
     hipEvent_t ev[2] = { nullptr, nullptr };
     bool used[2] = { false, false };        /* ev[i] was recorded */
@@ -307,6 +309,26 @@ int reserve(Ctx *c, size_t bytes) {
 
 size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+/* c's split workspace of at least bytes (made zero once when it grows;
+ * every split call leaves its counters zero). */
+int reserve_split(Ctx *c, size_t bytes) {
+    if (bytes <= c->skw_cap)
+        return PK_HIP_OK;
+    if (c->skw) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(c->skw);
+        c->skw = nullptr;
+        c->skw_cap = 0;
+    }
+    if (hipMalloc(&c->skw, bytes) != hipSuccess) {
+        c->skw = nullptr;
+        return fail(PK_HIP_ENOMEM, "hipMalloc of %zu bytes of split workspace failed", bytes);
+    }
+    PK_TRY(hipMemsetAsync(c->skw, 0, bytes, c->stream));
+    c->skw_cap = bytes;
+    return PK_HIP_OK;
+}
+
 int rmode_of_host() {
     switch (fegetround()) {
     case FE_TONEAREST: return 0;
@@ -387,7 +409,7 @@ int launch_product_siluq(const pk_hip_q8 *m, const pk_hip_act *a, const int8_t *
 
 int launch_product(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
                    const float *ws, const float *bias, const pk_hip_act *a, int add, int rmode,
-                   hipStream_t s, const int8_t *qp = nullptr) {
+                   hipStream_t s, const int8_t *qp = nullptr, void *skw = nullptr) {
     pkq8::GemmArgs g;
     g.w = m->w + (size_t)(r0 / 16) * pkq8::kUnitBytes;
     g.wstride = (uint64_t)(m->rows / 16) * pkq8::kUnitBytes;
@@ -401,6 +423,7 @@ int launch_product(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint3
     g.nb = a->n / a->qb;
     g.add = add;
     g.rmode = rmode;
+    g.skw = skw;
     pkq8::SegTable tab;
     tab.nseg = 1;
     tab.s[0] = pkq8::Seg{ out, qp ? qp : a->q, a->d, (uint64_t)os,
@@ -450,6 +473,10 @@ int pk_hip_tilings(void) { return pkq8::ring_count(); }
 const char *pk_hip_tiling_name(int index) { return pkq8::ring_name(index); }
 
 int pk_hip_force_tiling(int index) { return pkq8::set_ring(index); }
+
+int pk_hip_force_split(int splits) { return pkq8::set_skinny_split(splits); }
+
+size_t pk_hip_gemm_workspace(uint32_t rows) { return pkq8::skinny_workspace_bytes(rows); }
 
 int pk_hip_force_quantize(int kind) { return pkq8::set_quant_kernel(kind); }
 
@@ -660,7 +687,14 @@ int pk_hip_gemm_q8(float *out, size_t os, const int8_t *w, const float *ws, cons
     if (add && (e = h2d(l.c, dout, out, R * 4, T, os * 4)))
         return e;
     pk_hip_act da = { dq, dd, a->n, a->qb, a->T };
-    if ((e = launch_product(dout, R, m, r0, rows, wsd, bias ? db : nullptr, &da, add, rmode, s)))
+    /* few frames per row: the split over K, in the lease's own workspace */
+    void *skw = nullptr;
+    if (a->T <= 16 && a->qb == a->n) {
+        if ((e = reserve_split(l.c, pkq8::skinny_workspace_bytes(rows))))
+            return e;
+        skw = l.c->skw;
+    }
+    if ((e = launch_product(dout, R, m, r0, rows, wsd, bias ? db : nullptr, &da, add, rmode, s, nullptr, skw)))
         return e;
     return d2h(l.c, out, os * 4, dout, R * 4, T);
 }
@@ -751,6 +785,69 @@ int pk_hip_gemm_q8_packed_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_
     if ((e = check_panel(m, r0, rows, a->n)))
         return e;
     return launch_product(out, os, m, r0, rows, ws, bias, a, add, rmode, (hipStream_t)stream, qp);
+}
+
+static int check_work(const void *work, size_t work_bytes, uint32_t rows, const char *who) {
+    if (!work)
+        return PK_HIP_OK;
+    if ((uintptr_t)work & 255)
+        return fail(PK_HIP_EINVAL, "%s: the workspace must be 256-byte aligned", who);
+    const size_t need = pkq8::skinny_workspace_bytes(rows);
+    if (work_bytes < need)
+        return fail(PK_HIP_EINVAL, "%s: workspace of %zu bytes, %zu needed for %u rows", who, work_bytes, need, rows);
+    return PK_HIP_OK;
+}
+
+int pk_hip_gemm_q8_ws_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
+                          const float *ws, const float *bias, const pk_hip_act *a, int add, int rmode,
+                          void *work, size_t work_bytes, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!m)
+        return fail(PK_HIP_ENOTUP, "gemm_q8_ws_dev: no matrix");
+    if ((e = check_act(a, true)))
+        return e;
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!out || !ws)
+        return fail(PK_HIP_EINVAL, "gemm_q8_ws_dev: out or ws is NULL");
+    if ((uintptr_t)a->q & 15)
+        return fail(PK_HIP_EINVAL, "gemm_q8_ws_dev: a->q must be 16-byte aligned");
+    if (a->T > 1 && os < rows)
+        return fail(PK_HIP_EINVAL, "gemm_q8_ws_dev: output stride %zu is under rows %u", os, rows);
+    if (rmode < 0 || rmode > 3)
+        return fail(PK_HIP_EROUND, "gemm_q8_ws_dev: rmode %d", rmode);
+    if ((e = check_panel(m, r0, rows, a->n)) || (e = check_work(work, work_bytes, rows, "gemm_q8_ws_dev")))
+        return e;
+    return launch_product(out, os, m, r0, rows, ws, bias, a, add, rmode, (hipStream_t)stream, nullptr, work);
+}
+
+int pk_hip_gemm_q8_packed_ws_dev(float *out, size_t os, const pk_hip_q8 *m, uint32_t r0, uint32_t rows,
+                                 const float *ws, const float *bias, const pk_hip_act *a, const int8_t *qp,
+                                 int add, int rmode, void *work, size_t work_bytes, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if (!m)
+        return fail(PK_HIP_ENOTUP, "gemm_q8_packed_ws_dev: no matrix");
+    if (!a)
+        return fail(PK_HIP_EINVAL, "gemm_q8_packed_ws_dev: act is NULL");
+    if (a->T == 0)
+        return PK_HIP_OK;
+    if (!a->d || !qp || ((uintptr_t)qp & 15) || a->n % 32 || a->n > 16384 ||
+        !(a->qb == a->n || ((a->qb == 32 || a->qb == 64) && a->n % a->qb == 0)))
+        return fail(PK_HIP_EINVAL, "gemm_q8_packed_ws_dev: blocks of the whole row, 32 or 64 inputs, d and a "
+                                   "16-byte aligned qp");
+    if (!out || !ws)
+        return fail(PK_HIP_EINVAL, "gemm_q8_packed_ws_dev: out or ws is NULL");
+    if (a->T > 1 && os < rows)
+        return fail(PK_HIP_EINVAL, "gemm_q8_packed_ws_dev: output stride %zu is under rows %u", os, rows);
+    if (rmode < 0 || rmode > 3)
+        return fail(PK_HIP_EROUND, "gemm_q8_packed_ws_dev: rmode %d", rmode);
+    if ((e = check_panel(m, r0, rows, a->n)) || (e = check_work(work, work_bytes, rows, "gemm_q8_packed_ws_dev")))
+        return e;
+    return launch_product(out, os, m, r0, rows, ws, bias, a, add, rmode, (hipStream_t)stream, qp, work);
 }
 
 int pk_hip_gemm_q8_batch_dev(const pk_hip_job *jobs, uint32_t njobs, int rmode, void *stream) {

@@ -77,7 +77,19 @@ struct GemmArgs {
     /* 1: plain output stores; 0: non-temporal (set by the launch from the
      * size of its outputs, kPlainStoreBytes) */
     int plain = 0;
+    /* the skinny product's split-K workspace (skinny_workspace_bytes(rows),
+     * zero before its first use; every call leaves its counters zero), or
+     * null: no split */
+    void *skw = nullptr;
 };
+
+/* The skinny product split over K: at most kMaxSplit workgroups a panel; the
+ * workspace a product of rows channels needs (a counter a panel, then
+ * kMaxSplit partials of 1 KB a panel); forcing a split (1..kMaxSplit, -1 the
+ * heuristic; returns the one forced before). */
+constexpr uint32_t kMaxSplit = 8;
+size_t skinny_workspace_bytes(uint32_t rows);
+int set_skinny_split(int s);
 
 /* Outputs of a launch above this many bytes are stored plain. */
 constexpr uint64_t kPlainStoreBytes = (uint64_t)64 << 20;

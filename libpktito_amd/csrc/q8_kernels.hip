@@ -790,11 +790,26 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_q8_grouped_kernel(GemmArgs 
  * once. A workgroup takes one 16-row panel; its KW waves split the panel's
  * units between them, each reading its weight units straight from HBM (1 KB
  * contiguous a wave a unit) and the frames' inputs from L2, and their int32
- * sums meet in LDS. Per-row blocks only (MODE 0). */
-template <int KW, bool PACKED>
-__global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg sg) {
+ * sums meet in LDS. Per-row blocks only (MODE 0).
+ *
+ * SPLIT: S workgroups share a panel, each taking a run of its units (so a
+ * product of few panels still spreads its weights over many CUs). Each writes
+ * its exact int32 sums to the workspace's partials (agent-scope stores) and,
+ * once they are written, counts itself in at the panel's counter; the last
+ * one in reads the S partials back (agent-scope loads), adds them (integer
+ * sums: the same bits in any order), zeroes the counter for the next call,
+ * and runs ref's epilogue once. Workgroup b takes panel b % P8 (P8 the panels
+ * rounded up to 8) and split b / P8, so a panel's splits share an XCD (the
+ * hardware deals workgroup b to XCD b % 8) and meet in its L2. */
+template <int KW, bool PACKED, bool SPLIT>
+__global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg sg, uint32_t S, uint32_t P8,
+                                                                 int32_t *part, uint32_t *cnt) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t p = blockIdx.x, n = g.n, ku = g.ku, kr = g.kr, T = sg.T;
+    const uint32_t p = SPLIT ? blockIdx.x % P8 : blockIdx.x, si = SPLIT ? blockIdx.x / P8 : 0;
+    const uint32_t n = g.n, kr = g.kr, T = sg.T;
+    if (SPLIT && p >= g.rows / 16)
+        return;                                 /* padding up to a multiple of 8 panels */
+    const uint32_t ulo = SPLIT ? si * kr / S : 0, uhi = SPLIT ? (si + 1) * kr / S : kr;
     if (g.rmode)
         __builtin_amdgcn_s_setreg(2049, g.rmode);
     const int8_t *wp = g.w + (size_t)p * kUnitBytes + lane * 16;
@@ -819,20 +834,20 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
                 old[r] = o[r];
         }
     }
-    /* the wave's units u = wave + KW i, CU of them loaded at once (every
-     * load of a batch issued before its first MFMA: one memory round trip a
-     * batch, one batch for K <= 64 CU KW inputs); two accumulators so that
-     * consecutive MFMAs do not wait on each other (exact int32 sums). The
-     * weights, read once a call, load non-temporally: 8-11% sooner from
+    /* the wave's units u = ulo + wave + KW i, CU of them loaded at once
+     * (every load of a batch issued before its first MFMA: one memory round
+     * trip a batch, one batch for K <= 64 CU KW inputs); two accumulators so
+     * that consecutive MFMAs do not wait on each other (exact int32 sums).
+     * The weights, read once a call, load non-temporally: 8-11% sooner from
      * HBM (weights rotated over > 512 MB), the same when they are cached. */
     constexpr int CU = 8;
     v4i acc[2] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
-    for (uint32_t u0 = wave; u0 < kr; u0 += CU * KW) {
+    for (uint32_t u0 = ulo + wave; u0 < uhi; u0 += CU * KW) {
         v4i wv[CU], av[CU];
 #pragma unroll
         for (int i = 0; i < CU; i++) {
             const uint32_t u = u0 + i * KW;
-            if (u < kr) {
+            if (u < uhi) {
                 const uint32_t k = u * 64 + (lane >> 4) * 16;
                 wv[i] = __builtin_nontemporal_load((const v4i *)(wp + (size_t)u * ws_));
                 av[i] = *(const v4i *)(ap + (PACKED ? (size_t)u * sg.qstride : (k < n ? k : 0)));
@@ -840,7 +855,7 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
         }
 #pragma unroll
         for (int i = 0; i < CU; i++)
-            if (u0 + i * KW < kr)
+            if (u0 + i * KW < uhi)
                 acc[i & 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[i], av[i], acc[i & 1], 0, 0, 0);
     }
     __shared__ v4i red[KW][64];
@@ -852,6 +867,30 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
 #pragma unroll
     for (int w = 1; w < KW; w++)
         s += red[w][lane];
+    if constexpr (SPLIT) {
+        int32_t *mine = part + ((size_t)p * kMaxSplit + si) * 256 + lane * 4;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            __hip_atomic_store(mine + r, s[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        /* the partial has reached the coherence point before the count */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        uint32_t before = 0;
+        if (lane == 0)
+            before = __hip_atomic_fetch_add(cnt + p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        before = __builtin_amdgcn_readfirstlane(before);
+        if (before != S - 1)
+            return;
+        asm volatile("" ::: "memory");
+        const int32_t *all = part + (size_t)p * kMaxSplit * 256 + lane * 4;
+        v4i tot = { 0, 0, 0, 0 };
+        for (uint32_t k = 0; k < S; k++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                tot[r] += __hip_atomic_load(all + k * 256 + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+            __hip_atomic_store(cnt + p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s = tot;
+    }
     if (t >= T)
         return;
 #pragma unroll
@@ -861,6 +900,46 @@ __global__ __launch_bounds__(64 * KW) void gemm_q8_skinny_kernel(GemmArgs g, Seg
             v = v + br[r];
         store_out1(o + r, g.add ? old[r] + v : v, g.plain);
     }
+}
+
+static int g_forced_split = -1;
+
+int set_skinny_split(int s) {
+    const int was = g_forced_split;
+    g_forced_split = s >= 1 && s <= (int)kMaxSplit ? s : -1;
+    return was;
+}
+
+size_t skinny_workspace_bytes(uint32_t rows) {
+    const size_t panels = rows / 16;
+    return ((panels * 4 + 255) & ~(size_t)255) + panels * kMaxSplit * 1024;
+}
+
+/* How many workgroups share a panel. The hand-off through the workspace
+ * (agent-scope stores, the counter, the last one's loads) costs ~1.5-2 us, so
+ * a split pays only where one CU would stream a lot: measured (weights from
+ * HBM, each launch alone), 16 frames: K = 4096 5.2 us whole against 5.7 at
+ * two splits (1024 rows), K = 8192 8.2 against 6.3 at four (512 rows), K =
+ * 16384 14.2-14.8 against 7.6-8.9 at four; one frame: K = 4096 3.8 against
+ * 5.1 / 6.0 / 8.2 at two / four / eight, K = 16384 7.6-8.3 against 6.2-8.0 at
+ * four. So: the bytes a panel's workgroup streams (its weight units, and its
+ * frames' inputs from L2) at 192 KB or more take four splits, fewer take
+ * none (forced: any count up to one a unit). */
+static uint32_t skinny_splits(uint32_t panels, uint32_t kr, uint32_t T) {
+    uint32_t s;
+    if (g_forced_split > 0) {
+        s = (uint32_t)g_forced_split;
+    } else {
+        const uint64_t per = (uint64_t)kr * 1024 * (16 + (T < 16 ? T : 16)) / 16;
+        s = per >= (192u << 10) && panels * 4 <= 512 ? 4 : 1;
+        if (s > kr / 2)
+            s = 1;
+    }
+    if (s > kr)
+        s = kr;
+    if (s > kMaxSplit)
+        s = kMaxSplit;
+    return s < 1 ? 1 : s;
 }
 
 /* ----------------------------------------------- the pipelined product --
@@ -1885,17 +1964,38 @@ int launch_gemm(const GemmArgs &ga, const SegTable &tab, hipStream_t s, const ch
     if (mode == 0 && tab.nseg == 1 && tmax <= 16) {
         const uint32_t panels = g.rows / 16;
         const bool packed = tab.s[0].qstride != 0;
+        const uint32_t S = g.skw ? skinny_splits(panels, g.kr, tmax) : 1;
+        if (S > 1) {
+            /* the counters, then the partials (skinny_workspace_bytes) */
+            uint32_t *cnt = (uint32_t *)g.skw;
+            int32_t *part = (int32_t *)((char *)g.skw + (((size_t)panels * 4 + 255) & ~(size_t)255));
+            const uint32_t P8 = (panels + 7) / 8 * 8;
+            if (g.ku >= 32) {
+                if (packed)
+                    gemm_q8_skinny_kernel<8, true, true><<<P8 * S, 512, 0, s>>>(g, tab.s[0], S, P8, part, cnt);
+                else
+                    gemm_q8_skinny_kernel<8, false, true><<<P8 * S, 512, 0, s>>>(g, tab.s[0], S, P8, part, cnt);
+            } else {
+                if (packed)
+                    gemm_q8_skinny_kernel<4, true, true><<<P8 * S, 256, 0, s>>>(g, tab.s[0], S, P8, part, cnt);
+                else
+                    gemm_q8_skinny_kernel<4, false, true><<<P8 * S, 256, 0, s>>>(g, tab.s[0], S, P8, part, cnt);
+            }
+            snprintf(buf, sizeof buf, "%s<%d> split %u", packed ? "skinny_packed" : "skinny", g.ku >= 32 ? 8 : 4, S);
+            *name = buf;
+            return hipPeekAtLastError() == hipSuccess ? 0 : -1;
+        }
         if (g.ku >= 32) {
             if (packed)
-                gemm_q8_skinny_kernel<8, true><<<panels, 512, 0, s>>>(g, tab.s[0]);
+                gemm_q8_skinny_kernel<8, true, false><<<panels, 512, 0, s>>>(g, tab.s[0], 1, 0, nullptr, nullptr);
             else
-                gemm_q8_skinny_kernel<8, false><<<panels, 512, 0, s>>>(g, tab.s[0]);
+                gemm_q8_skinny_kernel<8, false, false><<<panels, 512, 0, s>>>(g, tab.s[0], 1, 0, nullptr, nullptr);
             *name = packed ? "skinny_packed<8>" : "skinny<8>";
         } else {
             if (packed)
-                gemm_q8_skinny_kernel<4, true><<<panels, 256, 0, s>>>(g, tab.s[0]);
+                gemm_q8_skinny_kernel<4, true, false><<<panels, 256, 0, s>>>(g, tab.s[0], 1, 0, nullptr, nullptr);
             else
-                gemm_q8_skinny_kernel<4, false><<<panels, 256, 0, s>>>(g, tab.s[0]);
+                gemm_q8_skinny_kernel<4, false, false><<<panels, 256, 0, s>>>(g, tab.s[0], 1, 0, nullptr, nullptr);
             *name = packed ? "skinny_packed<4>" : "skinny<4>";
         }
         return hipPeekAtLastError() == hipSuccess ? 0 : -1;

@@ -407,3 +407,122 @@ def test_quantize_reads_columns_at_a_stride(hip, torch, n, xs, qb):
             assert np.array_equal(qt2.cpu().numpy().reshape(-1), q), (n, xs, qbv, T)
             assert np.array_equal(bits(dt2.cpu().numpy()), bits(d)), (n, xs, qbv, T)
             assert np.array_equal(unpack_packed(qp.cpu().numpy(), n, T), q.reshape(T, n))
+
+
+SPLIT_SHAPES = [(M, K, N) for M in (1, 4, 16) for (K, N) in ((1024, 4096), (4096, 1024), (640, 1040))] + \
+    [(7, 96, 64), (16, 3136, 256)]
+
+
+@pytest.mark.parametrize("M,K,N", SPLIT_SHAPES)
+def test_split_few_frame_products(hip, torch, M, K, N):
+    """The few-frame products split over K (pk_hip_gemm_q8_ws_dev and its
+    packed form): under every forced split and the automatic one, row-major
+    and packed, with bias and add, a run of interior panels, os = 0 at one
+    frame, the bits of the unsplit entry, which the oracle pins here too;
+    two calls in a row on one workspace (the counters the first leaves must
+    be zero for the second), and the counters zero after every call."""
+    g = synth.rng(M * 13 + K + N)
+    w = synth.pack_q8(synth.weights(g, N, K))
+    ws = synth.scales(g, N)
+    bias = g.standard_normal(N).astype(np.float32)
+    x = synth.activations(g, M, K)
+    dev = torch.device("cuda")
+    xt = torch.from_numpy(x).to(dev)
+    qt = torch.empty((M, K), dtype=torch.int8, device=dev)
+    dt = torch.empty((M,), dtype=torch.float32, device=dev)
+    qp = torch.zeros((hip.packed_bytes(K, M),), dtype=torch.int8, device=dev)
+    hip.quantize_packed_dev(qt, qp, dt, xt, K, M, K)
+    r0 = 16 if N > 64 else 0
+    rows = N - r0
+    os_ = 0 if M == 1 else N + 3
+    bt = torch.from_numpy(bias).to(dev)
+    base = torch.from_numpy(g.standard_normal(max(1, M * os_ + N)).astype(np.float32)).to(dev)
+    q, d = ol.quantize(x.reshape(-1), M, K, K, K)
+    want_host = base.cpu().numpy().copy()
+    ol.gemm_q8(want_host, os_, w, ws, bias, rows, q, d, K, K, M, 1, r0=r0, threads=16)
+    work = torch.zeros((hip.gemm_workspace(rows),), dtype=torch.uint8, device=dev)
+    counters = (rows // 16 * 4 + 255) // 256 * 256        # a counter a panel, first in the workspace
+    with hip.Q8Matrix(w, ws) as m:
+        ref = base.clone()
+        hip.gemm_q8_dev(None, os_, m, r0, rows, None, bt[r0:], qt, dt, K, K, M, 1,
+                        ws_ptr=m.dev_scales + 4 * r0, out_ptr=ref.data_ptr() + 4 * r0)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(ref.cpu().numpy()), bits(want_host))
+        try:
+            for sp in (-1, 1, 2, 3, 4, 5, 8):
+                hip.force_split(sp)
+                for packed in (False, True):
+                    for call in range(2):
+                        out = base.clone()
+                        say("split product", M, K, N, sp, packed, call)
+                        if packed:
+                            hip.gemm_q8_packed_dev(None, os_, m, r0, rows, m.dev_scales + 4 * r0, bt[r0:], qp, dt,
+                                                   K, M, 1, out_ptr=out.data_ptr() + 4 * r0, work=work)
+                        else:
+                            hip.gemm_q8_dev(None, os_, m, r0, rows, None, bt[r0:], qt, dt, K, K, M, 1,
+                                            ws_ptr=m.dev_scales + 4 * r0, out_ptr=out.data_ptr() + 4 * r0,
+                                            work=work)
+                        torch.cuda.synchronize()
+                        kn = hip.last_kernel()
+                        assert np.array_equal(bits(out.cpu().numpy()), bits(want_host)), (sp, packed, call, kn)
+                        assert int(work[:counters].count_nonzero()) == 0, (sp, packed, call, kn)
+        finally:
+            hip.force_split(-1)
+
+
+def test_split_workspace_refusals(hip, torch):
+    """A workspace too small or misaligned is refused before anything runs."""
+    g = synth.rng(3)
+    w = synth.pack_q8(synth.weights(g, 1024, 256))
+    ws = synth.scales(g, 1024)
+    dev = torch.device("cuda")
+    q = torch.zeros((1, 256), dtype=torch.int8, device=dev)
+    d = torch.ones((1,), dtype=torch.float32, device=dev)
+    out = torch.zeros((1024,), dtype=torch.float32, device=dev)
+    need = hip.gemm_workspace(1024)
+    assert need >= 1024 // 16 * 8 * 1024
+    small = torch.zeros((need - 256,), dtype=torch.uint8, device=dev)
+    big = torch.zeros((need + 256,), dtype=torch.uint8, device=dev)
+    with hip.Q8Matrix(w, ws) as m:
+        with pytest.raises(hip.PkHipError):
+            hip.gemm_q8_dev(out, 0, m, 0, 1024, None, None, q, d, 256, 256, 1, 0, ws_ptr=m.dev_scales, work=small)
+        with pytest.raises(hip.PkHipError):
+            hip.gemm_q8_dev(None, 0, m, 0, 1024, None, None, q, d, 256, 256, 1, 0, ws_ptr=m.dev_scales,
+                            out_ptr=out.data_ptr(), work=big[16:])
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_split_deep_products_split_by_themselves(hip, torch, M):
+    """Deep few-panel products (K = 8192 into 512 channels at 16 frames, K =
+    16384 at one) take the split without forcing; their bits are the unsplit
+    entry's and, through the host entry (the lease's own workspace), the
+    oracle's."""
+    K = 8192 if M == 16 else 16384
+    N = 512
+    g = synth.rng(M + K)
+    w = synth.pack_q8(synth.weights(g, N, K))
+    ws = synth.scales(g, N)
+    x = synth.activations(g, M, K)
+    dev = torch.device("cuda")
+    xt = torch.from_numpy(x).to(dev)
+    qt = torch.empty((M, K), dtype=torch.int8, device=dev)
+    dt = torch.empty((M,), dtype=torch.float32, device=dev)
+    hip.quantize_dev(qt, dt, xt, K, K, M, K)
+    q, d = ol.quantize(x.reshape(-1), M, K, K, K)
+    want = np.zeros(M * N, np.float32)
+    ol.gemm_q8(want, N, w, ws, None, N, q, d, K, K, M, 0, threads=16)
+    work = torch.zeros((hip.gemm_workspace(N),), dtype=torch.uint8, device=dev)
+    with hip.Q8Matrix(w, ws) as m:
+        for call in range(2):
+            out = torch.zeros((M, N), dtype=torch.float32, device=dev)
+            say("deep split product", M, K, N, call)
+            hip.gemm_q8_dev(out, N, m, 0, N, None, None, qt, dt, K, K, M, 0, ws_ptr=m.dev_scales, work=work)
+            torch.cuda.synchronize()
+            assert "split 4" in hip.last_kernel(), hip.last_kernel()
+            assert np.array_equal(bits(out.cpu().numpy().reshape(-1)), bits(want)), call
+        host = np.zeros(M * N, np.float32)
+        say("deep split product, host entry", M, K, N)
+        hip.gemm_q8(host, N, w, ws, None, N, hip.make_act(q, d, K, K, M), 0)
+        assert "split" in hip.last_kernel(), hip.last_kernel()
+        assert np.array_equal(bits(host), bits(want))
