@@ -38,7 +38,6 @@ import json
 import os
 import sys
 import time
-from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -51,10 +50,6 @@ HBM_PEAK_GBS = 8000.0             # MI355X HBM3E, published
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
-
-
-def _addr(a):
-    return a.ctypes.data
 
 
 def parse():
@@ -723,6 +718,38 @@ def copy_calibration(torch):
     return {"copied_bytes": a.numel() * 4, "times": 3}
 
 
+def reference_pool(threads=16, seconds=1.0):
+    """The reference's own pool entries timed by its library (oracle/_ref's
+    dropin_cli --time-passes: pk_quantize_on then pk_gemm_on, 750 x 1024 ->
+    4096, THREADS pool threads, host pointers, PCIe inside each hip call),
+    unchanged (dropin_cli: 47 quantize items of 16 frames, 64-row slices of
+    the product) and with the core/passes.c change (dropin_cli_whole: one
+    call each under hip), on the hip table and on avx512-vnni."""
+    import subprocess
+    out = {}
+    for prog, key in (("dropin_cli", "pool_dealing"), ("dropin_cli_whole", "whole_product_change")):
+        path = os.path.join(ROOT, "oracle", "_ref", prog)
+        if not os.path.exists(path):
+            out[key] = "absent (the reference checkout was absent when the oracle was built)"
+            continue
+        res = {}
+        for table in ("hip", "avx512-vnni"):
+            env = dict(os.environ, PKTITO_KERNELS=table)
+            r = subprocess.run([path, "--time-passes", str(threads), str(seconds)], capture_output=True, text=True,
+                               env=env, timeout=300)
+            if r.returncode != 0:
+                res[table] = f"failed: {r.stderr.strip()[-300:]}"
+                continue
+            d = json.loads(r.stdout.strip().splitlines()[-1])
+            res[table] = dict(quantize_us=round(d["quantize_ms"] * 1e3, 1), gemm_q8_us=round(d["gemm_ms"] * 1e3, 1),
+                              tops=round(d["tops"], 2), calls=d["calls"], threads=d["threads"],
+                              table=d["table"].split(" (")[0], check=d["check"])
+        out[key] = res
+    out["note"] = ("host pointers through the reference's pool (core/passes.c), the hip table staging each call's "
+                   "activations and outputs over PCIe; the same outputs (check) on every table and dealing")
+    return out
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -1019,81 +1046,15 @@ def main():
 
         log("skinny done")
 
-        # the host-pointer drop-in (what backend/hip's table calls): host arrays
-        # in, host arrays out, every call staging activations and outputs over
-        # PCIe; the feed-forward up projection at M = 750
-        fu = next(p for p in prods if p.name == "ff1_up")
-        xh = fu.x_host.reshape(-1)
-        qh = np.zeros(fu.M * fu.K, np.int8)
-        dh = np.zeros(fu.M, np.float32)
-        oh = np.zeros(fu.M * fu.N, np.float32)
-        act = pk.make_act(qh, dh, fu.K, fu.K, fu.M)
-        pk.quantize(act, xh, fu.K)
-        pk.gemm_q8(oh, fu.N, fu.w, fu.ws, None, fu.N, act, 0)
-        reps = 20
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            pk.quantize(act, xh, fu.K)
-        tq = (time.perf_counter() - t0) / reps
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            pk.gemm_q8(oh, fu.N, fu.w, fu.ws, None, fu.N, act, 0)
-        tg = (time.perf_counter() - t0) / reps
-        # the same product dealt as the reference's pool deals it to 16
-        # threads (core/passes.c:28-46 and :80-109): quantize in 16-frame
-        # items, the product in slices of 64 or 256 rows, columns in chunks
-        # when that evens the last round; every call its own staging
-        nth = 16
-        pool = ThreadPoolExecutor(nth)
-        q_items = [(t0, min(16, fu.M - t0)) for t0 in range(0, fu.M, 16)]
-
-        def quant_item(it):
-            t0, nt = it
-            sub = pk.make_act(_addr(qh) + t0 * fu.K, _addr(dh) + 4 * t0, fu.K, fu.K, nt)
-            pk.quantize(sub, xh[t0 * fu.K:], fu.K)
-
-        step = 256 if fu.N // 256 >= 2 * nth else 64
-        rb = (fu.N + step - 1) // step
-        best, best_idle, best_all = 1, None, 1
-        for cc in range(1, 9):
-            if cc > 1 and fu.M // cc < 48:
-                break
-            items = rb * cc
-            alls = (items + nth - 1) // nth * nth
-            if best_idle is None or (alls - items) * best_all < best_idle * alls:
-                best, best_idle, best_all = cc, alls - items, alls
-        cstep = (fu.M + best - 1) // best
-        cstep = (cstep + 11) // 12 * 12 if best > 1 else fu.M
-        g_items = [(r0, min(step, fu.N - r0), c0, min(cstep, fu.M - c0))
-                   for c0 in range(0, fu.M, cstep) for r0 in range(0, fu.N, step)]
-
-        def gemm_item(it):
-            r0, nr, c0, nc = it
-            sub = pk.make_act(_addr(qh) + c0 * fu.K, _addr(dh) + 4 * c0, fu.K, fu.K, nc)
-            pk.gemm_q8(oh, fu.N, fu.w, fu.ws[r0:], None, nr, sub, 0, w_offset=r0 * fu.K,
-                       out_offset=c0 * fu.N + r0)
-
-        want = oh.copy()
-        list(pool.map(quant_item, q_items))
-        list(pool.map(gemm_item, g_items))
-        dealt_same = bool(np.array_equal(oh.view(np.uint32), want.view(np.uint32)))
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            list(pool.map(quant_item, q_items))
-        tpq = (time.perf_counter() - t0) / reps
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            list(pool.map(gemm_item, g_items))
-        tpg = (time.perf_counter() - t0) / reps
-        pool.shutdown()
-        extra["host_drop_in_ff1_up_M750"] = dict(
-            one_call=dict(quantize_us=round(tq * 1e6, 1), gemm_q8_us=round(tg * 1e6, 1),
-                          tops=round(fu.ops() / tg / 1e12, 2)),
-            pool16=dict(quantize_us=round(tpq * 1e6, 1), quantize_calls=len(q_items),
-                        gemm_q8_us=round(tpg * 1e6, 1), gemm_q8_calls=len(g_items),
-                        tops=round(fu.ops() / tpg / 1e12, 2), same_bits_as_one_call=dealt_same),
-            note="host pointers: x or q, d H2D and out D2H over PCIe inside each call, through pinned staging")
-        log("host drop-in done")
+        # the host-pointer drop-in inside the reference's own library: its
+        # pool entries pk_quantize_on / pk_gemm_on on the configs' first
+        # product, on the hip table and the reference's avx512-vnni, dealt
+        # as the unchanged core/passes.c deals them and with the
+        # whole-product change (part of the CPU-baseline leg: the programs
+        # are the reference's library built under oracle/_ref)
+        if not args.no_cpu:
+            extra["reference_pool_ff1_up_M750"] = reference_pool()
+            log("reference pool done")
         if not args.no_cpu:
             lc = cpu_baseline(host_inputs, args.cpu_seconds / 2)
             extra["layer_M750"]["cpu"] = {k: dict(tops=round(v["tops"], 4), cores=v["cores"], kind=v["kind"],

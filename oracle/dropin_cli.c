@@ -45,11 +45,31 @@
  * LSTM layer wx, wh (u32 rows, cols, i8 panels, f32 scales) and f32 b[4P];
  * jpred, f32 jpred_b[J]; jout, f32 jout_b[its rows]; jenc, f32 jenc_b[J]
  * (the joint's encoder half, f's product); u32 ntoks; i32 (id, frame, dur)
- * a token. */
+ * a token.
+ *
+ *   dropin_cli --time-passes THREADS SECONDS [M K N]
+ *
+ * needs no model: times the reference's own pool entries on a synthetic
+ * product (default M = 750 frames, K = 1024 inputs, N = 4096 rows, the
+ * configs' first shape: int8 weights uniform in [-127, 127] in PK_Q8 panels,
+ * scales uniform in [1e-3, 1e-2], frames N(0, 1) by Box-Muller from a fixed
+ * xorshift64* seed), on the table PKTITO_KERNELS names: pk_quantize_on
+ * (per-row blocks) then pk_gemm_on (no bias, no add, no callback) over a
+ * pool of THREADS, repeated until SECONDS have gone by, as the encoder makes
+ * them (core/encoder.c:63-77). Under PKTITO_KERNELS=hip the matrix is
+ * uploaded first, as a model's load does. Prints one JSON line: the table,
+ * the threads, the calls, and the quantize's, the product's and the pair's
+ * mean milliseconds. Built twice: _ref/dropin_cli (the pool's own dealing)
+ * and _ref/dropin_cli_whole (whole_product.c: one call a product under
+ * hip), so the two dealings time side by side. */
 #include "pktito.h"
 #include "model.h"
 #include "asr.h"
 #include "mel.h"
+#include "kernels.h"
+#include "os.h"
+#include "passes.h"
+#include "pool.h"
 
 #include <math.h>
 #include <stdio.h>
@@ -151,6 +171,10 @@ static int dump_decoder(const pk_model *m, const pk_asr *a, uint32_t Te, const c
 }
 
 int pk_hip_upload_model(const pk_model *m, char *err, size_t errlen);
+int pk_hip_upload_q8(const int8_t *q, const float *s, uint32_t rows, uint32_t cols);
+int pk_hip_release_q8(const int8_t *q);
+
+
 void pk_hip_release_model(const pk_model *m);
 
 static uint64_t g_s;
@@ -175,7 +199,77 @@ static int print_rows(void *arg, int64_t row, size_t n, const float *p) {
     return 0;
 }
 
+/* --time-passes (see the header) */
+static int time_passes(int threads, double secs, uint32_t M, uint32_t K, uint32_t N) {
+    if (threads < 1 || M == 0 || K % 32 || N % 16 || K > 16384)
+        return 2;
+    g_s = 0x9E3779B97F4A7C15ull * 7 + 1;
+    int8_t *w = malloc((size_t)N * K);
+    float *ws = malloc((size_t)N * sizeof *ws), *x = malloc((size_t)M * K * sizeof *x);
+    float *out = malloc((size_t)M * N * sizeof *out), *d = malloc((size_t)M * sizeof *d);
+    int8_t *q = malloc((size_t)M * K);
+    if (!w || !ws || !x || !out || !d || !q)
+        return 1;
+    /* PK_Q8: panels of 16 rows, groups of 4 inputs (core/pkf.h:28-41) */
+    for (uint32_t r = 0; r < N; r++)
+        for (uint32_t k = 0; k < K; k++)
+            w[((size_t)(r / 16) * (K / 4) + k / 4) * 64 + (r % 16) * 4 + k % 4] = (int8_t)(-127 + (int)(unit() * 255));
+    for (uint32_t r = 0; r < N; r++)
+        ws[r] = (float)(1e-3 + 9e-3 * unit());
+    for (size_t i = 0; i < (size_t)M * K; i += 2) {
+        const double u1 = unit() + 1e-300, u2 = unit(), rr = sqrt(-2 * log(u1));
+        x[i] = (float)(rr * cos(6.283185307179586 * u2));
+        if (i + 1 < (size_t)M * K)
+            x[i + 1] = (float)(rr * sin(6.283185307179586 * u2));
+    }
+    const char *want = getenv("PKTITO_KERNELS");
+    const int hip = want && !strcmp(want, "hip");
+    if (hip && pk_hip_upload_q8(w, ws, N, K)) {
+        fprintf(stderr, "upload failed\n");
+        return 1;
+    }
+    pk_pool *p = pk_pool_new(threads);
+    pk_q8 mat = { w, ws, N, K };
+    pk_act act = { q, d, K, K, M };
+    double tq = 0, tg = 0, t0 = pk_os_now();
+    long calls = 0;
+    /* one untimed pair first: the table's pick, the upload's first use */
+    pk_quantize_on(p, &act, x, K, M, K, K);
+    pk_gemm_on(p, out, N, &mat, NULL, &act, 0, NULL, NULL);
+    t0 = pk_os_now();
+    while (pk_os_now() - t0 < secs || calls < 3) {
+        const double a = pk_os_now();
+        pk_quantize_on(p, &act, x, K, M, K, K);
+        const double b = pk_os_now();
+        pk_gemm_on(p, out, N, &mat, NULL, &act, 0, NULL, NULL);
+        const double c = pk_os_now();
+        tq += b - a;
+        tg += c - b;
+        calls++;
+    }
+    double chk = 0;
+    for (size_t i = 0; i < (size_t)M * N; i += 997)
+        chk += out[i];
+    printf("{\"table\": \"%s\", \"threads\": %d, \"M\": %u, \"K\": %u, \"N\": %u, \"calls\": %ld, "
+           "\"quantize_ms\": %.4f, \"gemm_ms\": %.4f, \"pair_ms\": %.4f, \"tops\": %.4f, \"check\": %.6g}\n",
+           pk_k_name(), threads, M, K, N, calls, 1e3 * tq / calls, 1e3 * tg / calls, 1e3 * (tq + tg) / calls,
+           2.0 * M * K * N / (tg / calls) / 1e12, chk);
+    pk_pool_free(p);
+    if (hip)
+        pk_hip_release_q8(w);
+    free(w);
+    free(ws);
+    free(x);
+    free(out);
+    free(d);
+    free(q);
+    return 0;
+}
+
 int main(int argc, char **argv) {
+    if (argc >= 4 && !strcmp(argv[1], "--time-passes"))
+        return time_passes(atoi(argv[2]), atof(argv[3]), argc > 4 ? (uint32_t)atoi(argv[4]) : 750,
+                           argc > 5 ? (uint32_t)atoi(argv[5]) : 1024, argc > 6 ? (uint32_t)atoi(argv[6]) : 4096);
     if (argc < 6) {
         fprintf(stderr, "usage: %s MODEL.pkf SECONDS SEED FAST THREADS\n", argv[0]);
         return 2;

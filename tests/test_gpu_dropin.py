@@ -111,15 +111,18 @@ def test_kcheck_model_cases_on_tiny_pkf():
     assert all(f.startswith("FAIL tiny quantize: block of 0x1p-121") for f in hfails), hfails
 
 
+@pytest.mark.parametrize("whole", [0, 1])
 @pytest.mark.parametrize("seconds,seed,fast", [(20, 1, 0), (20, 2, 1), (7, 3, 0)])
-def test_transcript_on_the_hip_table_is_refs(seconds, seed, fast):
+def test_transcript_on_the_hip_table_is_refs(seconds, seed, fast, whole):
     """A transcription through the reference's unedited encoder and decoder
     (core/asr.c pk_asr_run, core/encoder.c, core/decoder.c) on 8 threads,
     whose pool deals the products to the table from every thread at once:
     the tokens and their frames and durations, byte for byte, are those of
     the run on ref; with the model uploaded at load and released before it
-    is freed. In blocks of 32 and, fast, of 64."""
-    cli = program("dropin_cli")
+    is freed. In blocks of 32 and, fast, of 64. whole 1: the harness built
+    with the core/passes.c change (oracle/whole_product.c), which hands the
+    table each product and each quantize whole."""
+    cli = program("dropin_cli_whole" if whole else "dropin_cli")
     outs = {}
     for table in ("ref", "hip"):
         say("transcript", table, seconds, seed, fast)
@@ -136,8 +139,9 @@ def test_transcript_on_the_hip_table_is_refs(seconds, seed, fast):
 TINY_DIAR = os.path.join(ROOT, "tests", "golden", "tiny-diar.pkf")
 
 
+@pytest.mark.parametrize("whole", [0, 1])
 @pytest.mark.parametrize("seconds,seed", [(20, 1), (40, 2)])
-def test_diarization_on_the_hip_table_is_refs(seconds, seed):
+def test_diarization_on_the_hip_table_is_refs(seconds, seed, whole):
     """The reference's second caller of the table: its diarizer (core/diar.c,
     pk_diar_run: the transformer layers' q, k, v, o and feed-forward
     products, the projection, the upsampling and the head, every one
@@ -146,8 +150,9 @@ def test_diarization_on_the_hip_table_is_refs(seconds, seed):
     on 8 threads. Every row of speaker probabilities, as exact hex floats,
     is the run on ref's; with the diarizer's matrices uploaded at load (the
     walker's diarizer branch) and released before the free. 40 s cross the
-    model's 27.2 s chunk, so the speaker cache carries between chunks."""
-    cli = program("dropin_cli")
+    model's 27.2 s chunk, so the speaker cache carries between chunks.
+    whole 1: with the core/passes.c change, as above."""
+    cli = program("dropin_cli_whole" if whole else "dropin_cli")
     outs = {}
     for table in ("ref", "hip"):
         say("diarization", table, seconds, seed)
@@ -160,3 +165,28 @@ def test_diarization_on_the_hip_table_is_refs(seconds, seed):
     last = outs["hip"].strip().splitlines()[-1].split()
     assert last[0] == "rows" and int(last[1]) >= seconds * 25 and int(last[2]) > 0, last
     assert outs["hip"] == outs["ref"]
+
+
+def test_whole_product_passes_time_through_the_pool():
+    """The reference's own pool entries (pk_quantize_on, pk_gemm_on) on a
+    synthetic 750 x 1024 -> 4096 product, through both harnesses on the hip
+    table and on ref's neighbour avx512-vnni: every run ends, the same
+    outputs (a checksum) on every table and dealing, and the whole-product
+    harness makes one call a product under hip (a handful of milliseconds at
+    most; the timings themselves are the bench's)."""
+    import json
+    res = {}
+    for whole in (0, 1):
+        cli = program("dropin_cli_whole" if whole else "dropin_cli")
+        for table in ("hip", "avx512-vnni"):
+            say("time passes", whole, table)
+            env = dict(os.environ, PKTITO_KERNELS=table)
+            r = subprocess.run([cli, "--time-passes", "8", "0.3"], capture_output=True, text=True, env=env,
+                               timeout=300)
+            if table != "hip" and r.returncode != 0 and "does not have" in r.stderr:
+                continue
+            assert r.returncode == 0, (whole, table, r.stderr[-2000:])
+            res[(whole, table)] = json.loads(r.stdout.strip().splitlines()[-1])
+    checks = {v["check"] for v in res.values()}
+    assert len(checks) == 1, res
+    assert res[(1, "hip")]["pair_ms"] < 5.0, res
