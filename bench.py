@@ -629,6 +629,24 @@ def decoder_steps(pk, torch, with_cpu, cpu_seconds=2.0):
         dd.tok_dur.cpu()
     out["joint_with_readback_us"] = round((time.perf_counter() - t0) / reps * 1e6, 2)
     out["launches"] = dict(predict=dec["L"] + 1, joint=2)
+    # the whole search in one launch (pk_hip_search_dev) over a minute of
+    # frames (750), synthetic frames at two scales (the larger emits more
+    # tokens); the call returns with the tokens on the host
+    V, blank, durs = dec["V"], dec["V"], [0, 1, 2, 3, 4]
+    T = 750
+    searches = []
+    for scale in (1.0, 2.0):
+        frames = (synth.rng(92).standard_normal((T, J)) * scale).astype(np.float32)
+        fd = torch.from_numpy(frames).cuda()
+        toks = dd.search(fd, T, blank, durs, 10)
+        reps = 5
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            dd.search(fd, T, blank, durs, 10)
+        ms = (time.perf_counter() - t0) / reps * 1e3
+        searches.append(dict(frames=T, scale=scale, tokens=len(toks), ms=round(ms, 3),
+                             us_per_frame=round(ms * 1e3 / T, 2), frames_host=frames, dev_toks=toks))
     dd.release()
     del gp, gj
     if with_cpu:
@@ -657,6 +675,32 @@ def decoder_steps(pk, torch, with_cpu, cpu_seconds=2.0):
         tj = (time.perf_counter() - t0) / n
         out["cpu_1_thread"] = dict(backend=impl, predict_us=round(tp * 1e6, 2), joint_us=round(tj * 1e6, 2),
                                    kind="reference" if impl != "oracle" else "port")
+        # the same searches on one host thread: their joints and predictions
+        # counted by running the search on the oracle's steps, each costed at
+        # the times above
+        from tdt_search import search as tdt
+        for sr in searches:
+            frames = sr["frames_host"]
+            cnt = {"j": 0, "p": 0}
+            st = {"h": np.zeros((dec["L"], dec["P"]), np.float32), "c": np.zeros((dec["L"], dec["P"]), np.float32),
+                  "gp": None}
+
+            def o_predict(k):
+                cnt["p"] += 1
+                st["h"], st["c"], st["gp"] = ol.predict(dw, k, st["h"], st["c"])
+
+            def o_joint(t):
+                cnt["j"] += 1
+                _, k, di = ol.joint(dw, frames[t], st["gp"])
+                return k, di
+            toks = tdt(T, o_predict, o_joint, blank, durs, 10)
+            sr["same_tokens_as_oracle_search"] = toks == sr["dev_toks"]
+            sr["joints"], sr["predictions"] = cnt["j"], cnt["p"]
+            sr["cpu_1_thread_ms"] = round((cnt["j"] * tj + cnt["p"] * tp) * 1e3, 3)
+    for sr in searches:
+        sr.pop("frames_host")
+        sr.pop("dev_toks")
+    out["search_one_launch"] = searches
     return out
 
 

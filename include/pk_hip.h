@@ -61,6 +61,7 @@ enum {
     PK_HIP_EDEVICE = 4,     /* a HIP call or a kernel launch failed */
     PK_HIP_ENOTUP = 5,      /* gemm_q8's w is inside no uploaded matrix */
     PK_HIP_EROUND = 6,      /* the caller's rounding mode is one this entry does not take */
+    PK_HIP_ETIMEOUT = 7,    /* a launch's bounded wait ran out (the launch ended, its results are not whole) */
 };
 
 /* The error code's name, and the calling thread's last error message. */
@@ -354,6 +355,39 @@ int pk_hip_lstm_step_dev(float *h_out, float *c, const float *h_in, const float 
  * index among the n_dur logits after them. */
 int pk_hip_joint_dev(float *logit, uint32_t *tok_dur, const pk_hip_q8 *jout, const float *jout_b, const float *f,
                      const float *gp, uint32_t V, uint32_t n_dur, void *stream);
+
+/* The decoder's weights on the device, for the search below: shapes and
+ * durations by value, the matrices uploaded, the vectors device pointers
+ * (core/model.h's prediction network and joint). */
+#define PK_HIP_DEC_MAX_LAYERS 8
+typedef struct {
+    uint32_t P, L, J, V, n_dur, blank, max_symbols;
+    int32_t  dur[64];                               /* n_dur <= 64 */
+    const float *embed;                             /* [V + 1][P] */
+    const pk_hip_q8 *wx[PK_HIP_DEC_MAX_LAYERS], *wh[PK_HIP_DEC_MAX_LAYERS];   /* [4P][P] */
+    const float *b[PK_HIP_DEC_MAX_LAYERS];          /* 4P each, or NULL */
+    const pk_hip_q8 *jpred, *jout;                  /* [J][P]; [rows][J], rows >= V + 1 + n_dur */
+    const float *jpred_b, *jout_b;
+} pk_hip_decoder;
+
+/* TDT's greedy search over a segment (core/decoder.c:121-147 and pk_decode,
+ * :158-173: the state zeroed, the blank's prediction first) in one launch on
+ * the device: the LSTM layers, jpred, the joint, its argmax, the duration
+ * step and the max_symbols rule, with no host round trip between frames.
+ * f: T frames of the joint's encoder half, device, [T][J] (pk_joint_frames'
+ * output). Returns once the search has ended, with *ntoks tokens in toks
+ * (host, 3 int32 a token: id, frame, duration, as pk_tok), the reference's
+ * tokens. cap must be at least T * max_symbols (the most a search can emit).
+ * ws: pk_hip_search_workspace(d, cap) bytes of device memory, 256-byte
+ * aligned. P and J multiples of 16 up to 1024, V + 1 <= 2048, L <= 8.
+ * spin_limit: the iterations a grid-wide wait may take before the launch
+ * gives up (0: the default, about a second); a launch that gives up ends
+ * and the call returns PK_HIP_ETIMEOUT. Not for stream capture (the launch
+ * is cooperative and the call synchronizes). No counterpart in the kernel
+ * table: core/decoder.c's loop, for a caller whose frames live in HBM. */
+size_t pk_hip_search_workspace(const pk_hip_decoder *d, uint32_t cap);
+int pk_hip_search_dev(const pk_hip_decoder *d, const float *f, uint32_t T, int32_t *toks, uint32_t cap,
+                      uint32_t *ntoks, void *ws, size_t ws_bytes, uint32_t spin_limit, void *stream);
 
 /* Measurement aids, with no counterpart in the reference: the floors a
  * small product's time is read against. pk_hip_empty_dev launches an empty

@@ -29,6 +29,7 @@ PK_HIP_ENOMEM = 3
 PK_HIP_EDEVICE = 4
 PK_HIP_ENOTUP = 5
 PK_HIP_EROUND = 6
+PK_HIP_ETIMEOUT = 7
 
 
 class PkHipError(RuntimeError):
@@ -55,6 +56,19 @@ class Job(ctypes.Structure):
     _fields_ = [("out", ctypes.c_void_p), ("os", ctypes.c_size_t), ("m", ctypes.c_void_p),
                 ("r0", ctypes.c_uint32), ("rows", ctypes.c_uint32), ("ws", ctypes.c_void_p),
                 ("bias", ctypes.c_void_p), ("a", Act), ("qp", ctypes.c_void_p), ("add", ctypes.c_int)]
+
+
+DEC_MAX_LAYERS = 8
+
+
+class Decoder(ctypes.Structure):
+    """pk_hip_decoder: the prediction network and joint for the device search."""
+    _fields_ = [("P", ctypes.c_uint32), ("L", ctypes.c_uint32), ("J", ctypes.c_uint32), ("V", ctypes.c_uint32),
+                ("n_dur", ctypes.c_uint32), ("blank", ctypes.c_uint32), ("max_symbols", ctypes.c_uint32),
+                ("dur", ctypes.c_int32 * 64), ("embed", ctypes.c_void_p),
+                ("wx", ctypes.c_void_p * DEC_MAX_LAYERS), ("wh", ctypes.c_void_p * DEC_MAX_LAYERS),
+                ("b", ctypes.c_void_p * DEC_MAX_LAYERS), ("jpred", ctypes.c_void_p), ("jout", ctypes.c_void_p),
+                ("jpred_b", ctypes.c_void_p), ("jout_b", ctypes.c_void_p)]
 
 
 _F32P = ctypes.c_void_p
@@ -142,6 +156,10 @@ _SIGS = {
     "pk_hip_gemv_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_int, ctypes.c_void_p]),
     "pk_hip_lstm_step_dev": (ctypes.c_int, [ctypes.c_void_p] * 7 + [ctypes.c_void_p]),
+    "pk_hip_search_workspace": (ctypes.c_size_t, [ctypes.POINTER(Decoder), ctypes.c_uint32]),
+    "pk_hip_search_dev": (ctypes.c_int, [ctypes.POINTER(Decoder), ctypes.c_void_p, ctypes.c_uint32,
+                                         ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32),
+                                         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_void_p]),
     "pk_hip_joint_dev": (ctypes.c_int, [ctypes.c_void_p] * 6 + [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]),
     "pk_hip_layer_dev": (ctypes.c_int, [ctypes.POINTER(LayerW), ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_size_t,
@@ -560,6 +578,36 @@ class DeviceDecoder:
         """core/decoder.c:81-101 at the frame whose encoder half is f."""
         joint_dev(self.logit, self.tok_dur, self.m["jout"], self.jout_b, f, self.gp, self.V, self.n_dur, stream,
                   f_ptr=f_ptr)
+
+    def search(self, f, T, blank, durs, max_symbols, spin_limit=0, stream=None, f_ptr=None):
+        """TDT's greedy search over T frames of the joint's encoder half f
+        (device [T, J]) in one launch (pk_hip_search_dev): the tokens as
+        (id, frame, duration). The state starts from zero, as the
+        reference's pk_decode starts a segment."""
+        d = Decoder()
+        d.P, d.L, d.J, d.V, d.n_dur = self.P, self.L, self.J, self.V, self.n_dur
+        d.blank, d.max_symbols = blank, max_symbols
+        for i, v in enumerate(durs):
+            d.dur[i] = int(v)
+        d.embed = self.embed.data_ptr()
+        for l in range(self.L):
+            d.wx[l] = self.m[f"wx{l}"].handle
+            d.wh[l] = self.m[f"wh{l}"].handle
+            d.b[l] = self.b[l].data_ptr()
+        d.jpred, d.jout = self.m["jpred"].handle, self.m["jout"].handle
+        d.jpred_b, d.jout_b = self.jpred_b.data_ptr(), self.jout_b.data_ptr()
+        cap = max(1, T * max_symbols)
+        nbytes = lib().pk_hip_search_workspace(ctypes.byref(d), cap)
+        if nbytes == 0:
+            raise PkHipError(PK_HIP_EINVAL, "search: shapes the device search does not take")
+        ws = self.torch.empty((nbytes + 256,), dtype=self.torch.uint8, device="cuda")
+        wp = (ws.data_ptr() + 255) // 256 * 256
+        toks = (ctypes.c_int32 * (3 * cap))()
+        n = ctypes.c_uint32(0)
+        fp = f_ptr if f_ptr is not None else _dptr(f)
+        _check(lib().pk_hip_search_dev(ctypes.byref(d), fp, T, toks, cap, ctypes.byref(n), wp, nbytes, spin_limit,
+                                       _stream(stream)))
+        return [(toks[3 * i], toks[3 * i + 1], toks[3 * i + 2]) for i in range(n.value)]
 
     def release(self):
         for m in self.m.values():

@@ -264,17 +264,16 @@ __global__ __launch_bounds__(64) void joint_kernel(float *__restrict__ logit, co
  * (loaded at once) and keeps its first maximum over non-NaN values, the runs
  * meet in order (ties to the earlier run, +0 and -0 equal as the comparison
  * has them), and a NaN at 0 wins. The durations are few: lane 0 scans them. */
-template <int RUN>
-__global__ __launch_bounds__(64) void argmax_kernel(uint32_t *__restrict__ tok_dur, const float *__restrict__ logit,
-                                                    uint32_t V, uint32_t n_dur) {
-    const int lane = threadIdx.x;
+template <int RUN, typename L>
+__device__ __forceinline__ void argmax_wave(L logit_at, uint32_t V, uint32_t n_dur, int lane, uint32_t &tok,
+                                            uint32_t &dur) {
     const uint32_t n = V + 1, run = (n + 63) / 64, a = lane * run;
     float lv[RUN];
 #pragma unroll
     for (int k = 0; k < RUN; k++)
-        lv[k] = k < (int)run && a + k < n ? logit[a + k] : 0.0f;
+        lv[k] = k < (int)run && a + k < n ? logit_at(a + k) : 0.0f;
     /* the durations' logits, lane i the i-th (up to 64), loaded with the run */
-    const float dv = lane < (int)n_dur ? logit[V + 1 + lane] : 0.0f;
+    const float dv = lane < (int)n_dur ? logit_at(V + 1 + lane) : 0.0f;
     float bv = 0.0f;
     int bi = -1;
 #pragma unroll
@@ -304,16 +303,276 @@ __global__ __launch_bounds__(64) void argmax_kernel(uint32_t *__restrict__ tok_d
                 bdv = x;
             }
         }
-    } else if (lane == 0) {
-        for (uint32_t i = 1; i < n_dur; i++)
-            if (logit[V + 1 + i] > logit[V + 1 + bd])
-                bd = i;
+    } else {
+        if (lane == 0)
+            for (uint32_t i = 1; i < n_dur; i++)
+                if (logit_at(V + 1 + i) > logit_at(V + 1 + bd))
+                    bd = i;
+        bd = __shfl(bd, 0);
     }
-    if (lane == 0) {
-        const float l0 = lv[0];                  /* lane 0's run starts at token 0 */
-        const uint32_t best = l0 != l0 || bi < 0 ? 0u : (uint32_t)bi;
-        tok_dur[0] = best;
-        tok_dur[1] = bd;
+    const float l0 = __shfl(lv[0], 0);          /* lane 0's run starts at token 0 */
+    const int b0 = __shfl(bi, 0);
+    tok = l0 != l0 || b0 < 0 ? 0u : (uint32_t)b0;
+    dur = bd;
+}
+
+template <int RUN>
+__global__ __launch_bounds__(64) void argmax_kernel(uint32_t *__restrict__ tok_dur, const float *__restrict__ logit,
+                                                    uint32_t V, uint32_t n_dur) {
+    uint32_t tok, dur;
+    argmax_wave<RUN>([&](uint32_t i) { return logit[i]; }, V, n_dur, threadIdx.x, tok, dur);
+    if (threadIdx.x == 0) {
+        tok_dur[0] = tok;
+        tok_dur[1] = dur;
+    }
+}
+
+/* ------------------------------------------------------- the search -- *
+ *
+ * TDT's greedy search (core/decoder.c:121-147) over a segment's frames in one
+ * launch: the prediction (the label's embedding through the LSTM layers and
+ * jpred, :65-79), the joint and its argmax (:81-101), the duration step, the
+ * max_symbols rule and the token list, with every state (h, c of each layer,
+ * gp, the logits, the frame, the tokens) in HBM and registers, so the host
+ * reads nothing between frames.
+ *
+ * Every workgroup runs the same control flow. A phase (an LSTM layer's step,
+ * jpred, the joint's logits) splits its rows over the workgroups as the
+ * one-launch kernels above split them, and ends at a grid barrier; after the
+ * joint's barrier every workgroup reads all the logits and makes the same
+ * argmax, so all of them take the same branch of the search and meet at the
+ * same barriers. What one workgroup writes and another reads (h, gp, the
+ * logits) goes through agent-scope atomic stores and loads, coherent across
+ * the XCDs' L2s, and so does c, which the workgroup that steps it reads
+ * back a token later. The launch is
+ * cooperative (every workgroup resident at once), and every barrier's wait is
+ * bounded: past its iteration limit a workgroup raises the error flag and
+ * leaves, and the others see the flag in their waits and leave too, so a
+ * launch always ends; the host reads the flag. The bits are the one-launch
+ * kernels' (the same helpers in the same order), so the reference's. */
+
+__device__ __forceinline__ float cload(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void cstore(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* chunk i of a row of n floats read coherently, zeros past n */
+__device__ __forceinline__ float4 crow4(const float *x, uint32_t i, uint32_t n) {
+    const uint32_t k = 4 * i;
+    return make_float4(k < n ? cload(x + k) : 0.0f, k + 1 < n ? cload(x + k + 1) : 0.0f,
+                       k + 2 < n ? cload(x + k + 2) : 0.0f, k + 3 < n ? cload(x + k + 3) : 0.0f);
+}
+
+template <int CH, int KU>
+__global__ __launch_bounds__(256) void search_kernel(SearchArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t q0[64 * KU], q1[64 * KU];
+    __shared__ float dq[2], gates[4][16];
+    __shared__ uint32_t shared_u[3];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t G = gridDim.x, wg = blockIdx.x;
+    const uint32_t P = a.P, J = a.J;
+    uint32_t nbar = 0;
+
+    /* the grid barrier: this workgroup's stores have landed, then it counts
+     * itself in and waits for the G arrivals of barrier nbar; false (leave)
+     * on the error flag or past the iteration limit */
+    auto barrier = [&]() -> bool {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        nbar++;
+        if (wv == 0) {
+            /* each workgroup stores the barrier's number to its own slot;
+             * wave 0 reads every slot in one load (lane i slot i, G <= 64)
+             * until all of them hold it: no two workgroups update one word */
+            uint32_t *slot = a.sync + 64;
+            if (lane == 0)
+                __hip_atomic_store(slot + wg, nbar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint32_t it = 0, bad = 0;
+            while (true) {
+                const uint32_t v = lane < (int)G ? __hip_atomic_load(slot + lane, __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT) : nbar;
+                if (__builtin_amdgcn_read_exec() == __ballot(v >= nbar))
+                    break;
+                if (++it >= a.spin || ((it & 15) == 0 &&
+                                       __hip_atomic_load(a.sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+                    bad = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (bad && lane == 0)
+                __hip_atomic_store(a.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0)
+                shared_u[2] = bad;
+        }
+        __syncthreads();
+        return shared_u[2] == 0;
+    };
+
+    /* one LSTM layer's step on units 16 wg .. + 15 (lstm_kernel's steps):
+     * x, h_in and c read, c and h_out stored, all through the coherent
+     * accessors (c is this workgroup's own, read back a token later) */
+    auto lstm = [&](uint32_t l, const float *x, const float *h_in, float *h_out) {
+        if (wg >= P / 16)
+            return;
+        float *c = a.c + (size_t)l * P;
+        const uint32_t j0 = 16 * wg;
+        float4 v[CH];
+        if (wv == 0)
+            load_row<CH>([&](uint32_t i) { return crow4(x, i, P); }, P, lane, v);
+        else if (wv == 1)
+            load_row<CH>([&](uint32_t i) { return crow4(h_in, i, P); }, P, lane, v);
+        const uint32_t pn = (wv * P + j0) / 16;
+        v4i wxv[KU], whv[KU];
+        panel_load<KU>(a.wx[l], a.lstm_stride, pn, a.kr_p, lane, wxv);
+        panel_load<KU>(a.wh[l], a.lstm_stride, pn, a.kr_p, lane, whv);
+        const uint32_t r = wv * P + j0 + (lane & 15);
+        const float wxsr = a.wxs[l][r], whsr = a.whs[l][r], br = a.b[l] ? a.b[l][r] : 0.0f;
+        const float cold = threadIdx.x < 16 ? cload(c + j0 + threadIdx.x) : 0.0f;
+        if (wv == 0) {
+            const float d = quant_loaded<CH>(v, P, a.kr_p, q0, lane);
+            if (lane == 0)
+                dq[0] = d;
+        } else if (wv == 1) {
+            const float d = quant_loaded<CH>(v, P, a.kr_p, q1, lane);
+            if (lane == 0)
+                dq[1] = d;
+        }
+        __syncthreads();
+        const int sx = panel_sum<KU>(wxv, a.kr_p, q0, lane);
+        const int sh = panel_sum<KU>(whv, a.kr_p, q1, lane);
+        if (lane < 16) {
+            const float g = gemv_out(sx, dq[0], wxsr, a.b[l], br);
+            gates[wv][lane] = g + gemv_out(sh, dq[1], whsr, nullptr, 0.0f);
+        }
+        __syncthreads();
+        if (threadIdx.x < 16) {
+            const uint32_t t = threadIdx.x, j = j0 + t;
+            const float i = pk_sigmoidf(gates[0][t]);
+            const float f = pk_sigmoidf(gates[1][t]);
+            const float u = pk_tanhf(gates[2][t]);
+            const float o = pk_sigmoidf(gates[3][t]);
+            const float cj = f * cold + i * u;
+            cstore(c + j, cj);
+            cstore(h_out + j, o * pk_tanhf(cj));
+        }
+    };
+
+    /* a row of n inputs (value4 gives its chunks) quantized once by wave 0,
+     * then one 16-row panel of w a wave (panel 4 wg + wave, those below
+     * panels): gemv_out into out, stored coherently */
+    auto gemv = [&](auto value4, uint32_t n, uint32_t kr, const int8_t *w, uint64_t stride, const float *ws,
+                    const float *bias, uint32_t panels, float *out) {
+        const uint32_t pn = 4 * wg + wv;
+        const bool mine = pn < panels;
+        float4 v[CH];
+        if (wv == 0)
+            load_row<CH>(value4, n, lane, v);
+        v4i wvv[KU];
+        if (mine)
+            panel_load<KU>(w, stride, pn, kr, lane, wvv);
+        const uint32_t r = 16 * pn + (lane & 15);
+        const float wsr = mine ? ws[r] : 0.0f, br = mine && bias ? bias[r] : 0.0f;
+        if (wv == 0) {
+            const float d = quant_loaded<CH>(v, n, kr, q0, lane);
+            if (lane == 0)
+                dq[0] = d;
+        }
+        __syncthreads();
+        if (mine) {
+            const int s = panel_sum<KU>(wvv, kr, q0, lane);
+            if (lane < 16)
+                cstore(out + r, gemv_out(s, dq[0], wsr, bias, br));
+        }
+    };
+
+    uint32_t cur = 0;                               /* bit l: which of layer l's two h buffers is current */
+    auto predict = [&](uint32_t label) -> bool {
+        const float *x = a.embed + (size_t)label * P;
+        for (uint32_t l = 0; l < a.L; l++) {
+            const uint32_t c0 = (cur >> l) & 1;
+            const float *h_in = a.h + ((size_t)l * 2 + c0) * P;
+            float *h_out = a.h + ((size_t)l * 2 + (c0 ^ 1)) * P;
+            lstm(l, x, h_in, h_out);
+            cur ^= 1u << l;
+            if (!barrier())
+                return false;
+            x = h_out;
+        }
+        const float *hl = x;
+        gemv([&](uint32_t i) { return crow4(hl, i, P); }, P, a.kr_p, a.jpred, a.jpred_stride, a.jpred_s,
+             a.jpred_b, J / 16, a.gp);
+        return barrier();
+    };
+
+    /* the joint at frame t: relu(f + gp) quantized, jout's panels, then every
+     * workgroup's wave 0 takes the argmax of all the logits */
+    auto joint = [&](uint32_t t, uint32_t &k, uint32_t &di) -> bool {
+        const float *ft = a.f + (size_t)t * J;
+        gemv([&](uint32_t i) {
+                 const float4 fv = row4<false>(ft, i, J), gv = crow4(a.gp, i, J);
+                 return make_float4(relu_sum(fv.x, gv.x), relu_sum(fv.y, gv.y), relu_sum(fv.z, gv.z),
+                                    relu_sum(fv.w, gv.w));
+             },
+             J, a.kr_j, a.jout, a.jout_stride, a.jout_s, a.jout_b, a.rows_out / 16, a.logit);
+        if (!barrier())
+            return false;
+        if (wv == 0) {
+            uint32_t tk, dd;
+            argmax_wave<32>([&](uint32_t i) { return cload(a.logit + i); }, a.V, a.n_dur, lane, tk, dd);
+            if (lane == 0) {
+                shared_u[0] = tk;
+                shared_u[1] = dd;
+            }
+        }
+        __syncthreads();
+        k = shared_u[0];
+        di = shared_u[1];
+        __syncthreads();
+        return true;
+    };
+
+    const uint32_t T = a.T, blank = a.blank;
+    uint32_t ntoks = 0, status = 0;
+    if (!predict(blank))
+        return;
+    uint32_t t = 0, last = 0xffffffffu, lasts = 0;
+    while (t < T) {
+        uint32_t k, di, d, at;
+        do {
+            at = t;
+            if (!joint(t, k, di))
+                return;
+            d = (uint32_t)a.dur[di];
+            if (k == blank && d == 0)
+                d = 1;
+            t += d;
+        } while (k == blank && t < T);
+        if (k == blank)
+            break;
+        if (ntoks == a.cap) {
+            status = 2;
+            break;
+        }
+        if (wg == 0 && threadIdx.x == 0) {
+            a.toks[3 * ntoks] = (int32_t)k;
+            a.toks[3 * ntoks + 1] = (int32_t)at;
+            a.toks[3 * ntoks + 2] = a.dur[di];
+        }
+        ntoks++;
+        lasts = last == at ? lasts + 1 : 1;
+        last = at;
+        if (!predict(k))
+            return;
+        if (lasts >= a.max_symbols && last == t)
+            t++;
+    }
+    if (wg == 0 && threadIdx.x == 0) {
+        a.out[0] = ntoks;
+        a.out[1] = status;
     }
 }
 
@@ -383,6 +642,49 @@ int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstr
     else
         argmax_kernel<64><<<1, 64, 0, s>>>(tok_dur, logit, V, n_dur);
     return hipPeekAtLastError() == hipSuccess ? 0 : -1;
+}
+
+size_t search_workspace_bytes(uint32_t L, uint32_t P, uint32_t J, uint32_t rows_out, uint32_t cap) {
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    return up(512) + up((size_t)L * 2 * P * 4) + up((size_t)L * P * 4) + up((size_t)J * 4) + up((size_t)rows_out * 4) +
+           up((size_t)cap * 12) + up(8);
+}
+
+int launch_search(SearchArgs &a, void *ws, hipStream_t s) {
+    if (a.P == 0 || a.P % 16 || a.P > 1024 || a.J == 0 || a.J % 16 || a.J > 1024 || a.L == 0 ||
+        a.L > (uint32_t)kMaxDecLayers || a.rows_out % 16 || a.V + 1 + a.n_dur > a.rows_out || a.n_dur == 0 ||
+        a.n_dur > 64 || a.V + 1 > 64 * 32 || 64 * a.kr_p < a.P || a.kr_p > 16 || 64 * a.kr_j < a.J || a.kr_j > 16)
+        return -2;
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    char *p = (char *)ws;
+    a.sync = (uint32_t *)p;
+    p += up(512);
+    a.h = (float *)p;
+    p += up((size_t)a.L * 2 * a.P * 4);
+    a.c = (float *)p;
+    p += up((size_t)a.L * a.P * 4);
+    a.gp = (float *)p;
+    p += up((size_t)a.J * 4);
+    a.logit = (float *)p;
+    p += up((size_t)a.rows_out * 4);
+    a.toks = (int32_t *)p;
+    p += up((size_t)a.cap * 12);
+    a.out = (uint32_t *)p;
+    /* the arrivals, the flag and the state start at zero (c and h: the
+     * reference zeroes them a segment, core/decoder.c:158-165); the logits,
+     * gp and the tokens are written before they are read */
+    if (hipMemsetAsync(a.sync, 0, 512, s) != hipSuccess ||
+        hipMemsetAsync(a.h, 0, up((size_t)a.L * 2 * a.P * 4) + up((size_t)a.L * a.P * 4), s) != hipSuccess ||
+        hipMemsetAsync(a.out, 0, 8, s) != hipSuccess)
+        return -1;
+    uint32_t G = a.P / 16;
+    G = G > (a.rows_out / 16 + 3) / 4 ? G : (a.rows_out / 16 + 3) / 4;
+    G = G > (a.J / 16 + 3) / 4 ? G : (a.J / 16 + 3) / 4;
+    if (G > 64)
+        return -2;                              /* the barrier reads every workgroup's slot in one wave */
+    void *args[] = { &a };
+    const hipError_t e = hipLaunchCooperativeKernel((const void *)search_kernel<4, 16>, dim3(G), dim3(256), args, 0, s);
+    return e == hipSuccess ? 0 : -1;
 }
 
 }  // namespace pkq8

@@ -460,6 +460,7 @@ const char *pk_hip_strerror(int err) {
     case PK_HIP_EDEVICE: return "HIP error";
     case PK_HIP_ENOTUP: return "matrix not uploaded";
     case PK_HIP_EROUND: return "unsupported rounding mode";
+    case PK_HIP_ETIMEOUT: return "a bounded wait on the device ran out";
     default: return "unknown error";
     }
 }
@@ -1312,6 +1313,100 @@ int pk_hip_joint_dev(float *logit, uint32_t *tok_dur, const pk_hip_q8 *jout, con
                                  (hipStream_t)stream),
               "joint launch");
     g_kernel = "joint";
+    return PK_HIP_OK;
+}
+
+static int search_shape(const pk_hip_decoder *d) {
+    if (!d || !d->embed || !d->jpred || !d->jout || d->L == 0 || d->L > PK_HIP_DEC_MAX_LAYERS || d->n_dur == 0 ||
+        d->n_dur > 64 || d->P == 0 || d->P % 16 || d->P > 1024 || d->J == 0 || d->J % 16 || d->J > 1024 ||
+        d->V + 1 > 2048 || d->blank > d->V || d->max_symbols == 0)
+        return fail(PK_HIP_EINVAL, "search: P and J multiples of 16 up to 1024, 1 <= L <= %d, 1 <= n_dur <= 64, "
+                                   "V + 1 <= 2048, blank <= V, max_symbols >= 1, embed, jpred and jout set",
+                    PK_HIP_DEC_MAX_LAYERS);
+    for (uint32_t l = 0; l < d->L; l++) {
+        const pk_hip_q8 *x = d->wx[l], *h = d->wh[l];
+        if (!x || !h || x->rows != 4 * d->P || x->cols != d->P || h->rows != 4 * d->P || h->cols != d->P)
+            return fail(PK_HIP_EINVAL, "search: layer %u's wx and wh must be uploaded [4P][P] matrices", l);
+    }
+    if (d->jpred->rows != d->J || d->jpred->cols != d->P || d->jout->cols != d->J ||
+        d->V + 1 + d->n_dur > d->jout->rows)
+        return fail(PK_HIP_EINVAL, "search: jpred [J][P], jout [rows][J] with rows >= V + 1 + n_dur");
+    return PK_HIP_OK;
+}
+
+size_t pk_hip_search_workspace(const pk_hip_decoder *d, uint32_t cap) {
+    if (search_shape(d))
+        return 0;
+    return pkq8::search_workspace_bytes(d->L, d->P, d->J, d->jout->rows, cap);
+}
+
+int pk_hip_search_dev(const pk_hip_decoder *d, const float *f, uint32_t T, int32_t *toks, uint32_t cap,
+                      uint32_t *ntoks, void *ws, size_t ws_bytes, uint32_t spin_limit, void *stream) {
+    int e = pk_hip_init();
+    if (e)
+        return e;
+    if ((e = search_shape(d)))
+        return e;
+    if (!ntoks || (T && (!f || !toks)))
+        return fail(PK_HIP_EINVAL, "search: f, toks and ntoks set");
+    *ntoks = 0;
+    if (T == 0)
+        return PK_HIP_OK;
+    if ((uint64_t)cap < (uint64_t)T * d->max_symbols)
+        return fail(PK_HIP_EINVAL, "search: cap %u is under T * max_symbols = %llu", cap,
+                    (unsigned long long)T * d->max_symbols);
+    const size_t need = pkq8::search_workspace_bytes(d->L, d->P, d->J, d->jout->rows, cap);
+    if (!ws || ((uintptr_t)ws & 255) || ws_bytes < need)
+        return fail(PK_HIP_EINVAL, "search: a 256-byte aligned workspace of %zu bytes (%zu given)", need, ws_bytes);
+    pkq8::SearchArgs a{};
+    a.f = f;
+    a.embed = d->embed;
+    for (uint32_t l = 0; l < d->L; l++) {
+        a.wx[l] = d->wx[l]->w;
+        a.wh[l] = d->wh[l]->w;
+        a.wxs[l] = d->wx[l]->s;
+        a.whs[l] = d->wh[l]->s;
+        a.b[l] = d->b[l];
+    }
+    a.jpred = d->jpred->w;
+    a.jout = d->jout->w;
+    a.jpred_s = d->jpred->s;
+    a.jout_s = d->jout->s;
+    a.jpred_b = d->jpred_b;
+    a.jout_b = d->jout_b;
+    a.lstm_stride = (uint64_t)(4 * d->P / 16) * pkq8::kUnitBytes;
+    a.jpred_stride = (uint64_t)(d->J / 16) * pkq8::kUnitBytes;
+    a.jout_stride = (uint64_t)(d->jout->rows / 16) * pkq8::kUnitBytes;
+    a.P = d->P;
+    a.L = d->L;
+    a.J = d->J;
+    a.V = d->V;
+    a.n_dur = d->n_dur;
+    a.rows_out = d->jout->rows;
+    a.blank = d->blank;
+    a.max_symbols = d->max_symbols;
+    a.T = T;
+    a.cap = cap;
+    a.kr_p = pkq8::units_with_data(d->P);
+    a.kr_j = pkq8::units_with_data(d->J);
+    a.spin = spin_limit ? spin_limit : 1u << 22;
+    for (uint32_t i = 0; i < d->n_dur; i++)
+        a.dur[i] = d->dur[i];
+    hipStream_t s = (hipStream_t)stream;
+    PK_LAUNCH(pkq8::launch_search(a, ws, s), "search launch");
+    g_kernel = "search";
+    uint32_t res[2] = { 0, 0 }, flag[2] = { 0, 0 };
+    PK_TRY(hipMemcpyAsync(res, a.out, sizeof res, hipMemcpyDeviceToHost, s));
+    PK_TRY(hipMemcpyAsync(flag, a.sync, sizeof flag, hipMemcpyDeviceToHost, s));
+    PK_TRY(hipStreamSynchronize(s));
+    if (flag[1])
+        return fail(PK_HIP_ETIMEOUT, "search: a grid-wide wait ran past its %u iterations; the launch left early",
+                    a.spin);
+    if (res[1] == 2 || res[0] > cap)
+        return fail(PK_HIP_EINVAL, "search: more than cap %u tokens", cap);
+    if (res[0])
+        PK_TRY(hipMemcpy(toks, a.toks, (size_t)res[0] * 12, hipMemcpyDeviceToHost));
+    *ntoks = res[0];
     return PK_HIP_OK;
 }
 

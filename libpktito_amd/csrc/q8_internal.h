@@ -166,6 +166,35 @@ int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstr
                  const float *bias, const float *f, const float *gp, uint32_t rows, uint32_t J, uint32_t kr,
                  uint32_t V, uint32_t n_dur, hipStream_t s);
 
+/* The decoder's greedy search in one cooperative launch (dec_kernels.hip):
+ * the launch's arguments, the caller filling everything above the
+ * workspace's pieces; launch_search carves ws (search_workspace_bytes),
+ * zeroes the arrivals, the flag and the state on s, and launches. 0, -2 for
+ * shapes it does not take, -1 for a failed call. */
+constexpr int kMaxDecLayers = 8;
+
+struct SearchArgs {
+    const float *f;                                 /* [T][J], the joint's encoder half of each frame */
+    const float *embed;                             /* [V + 1][P] */
+    const int8_t *wx[kMaxDecLayers], *wh[kMaxDecLayers];
+    const float *wxs[kMaxDecLayers], *whs[kMaxDecLayers], *b[kMaxDecLayers];
+    const int8_t *jpred, *jout;
+    const float *jpred_s, *jpred_b, *jout_s, *jout_b;
+    uint64_t lstm_stride, jpred_stride, jout_stride; /* the matrices' unit strides */
+    uint32_t P, L, J, V, n_dur, rows_out, blank, max_symbols, T, cap, kr_p, kr_j, spin;
+    int32_t dur[64];
+    uint32_t *sync;                                 /* [1] the error flag, [64 + b] workgroup b's last barrier: zero at launch */
+    float *h;                                       /* [L][2][P], zero at launch */
+    float *c;                                       /* [L][P], zero at launch */
+    float *gp;                                      /* [J] */
+    float *logit;                                   /* [rows_out] */
+    int32_t *toks;                                  /* [cap][3]: token, frame, duration */
+    uint32_t *out;                                  /* [0] tokens, [1] 0, or 2 when cap was reached */
+};
+
+size_t search_workspace_bytes(uint32_t L, uint32_t P, uint32_t J, uint32_t rows_out, uint32_t cap);
+int launch_search(SearchArgs &a, void *ws, hipStream_t s);
+
 /* Measurement aids (diag_kernels.hip): an empty launch; a streaming read of
  * bytes (a multiple of 16) at p, 16-byte aligned. */
 int launch_empty(hipStream_t s);

@@ -215,3 +215,64 @@ def test_greedy_search_on_device(hip, torch):
     finally:
         dd.release()
     assert got == want and len(want) > 3
+
+
+@pytest.mark.parametrize("T,seed,scale", [(60, 16, 2.0), (300, 21, 1.0), (5, 22, 3.0)])
+def test_search_in_one_launch(hip, torch, T, seed, scale):
+    """pk_hip_search_dev, the whole search in one cooperative launch, at the
+    model's shapes (pred 640, 2 LSTM layers, joint 640, 1024 tokens + blank,
+    5 durations): the oracle-driven search's tokens, frames and durations;
+    over frames whose scale makes it emit often and others that are mostly
+    blank; then the same search again on the same decoder (the state starts
+    from zero each call)."""
+    dec = decoder(seed, True)
+    V, J, L, P = dec["V"], dec["J"], dec["L"], dec["P"]
+    durs = [0, 1, 2, 3, 4]
+    g = synth.rng(seed + 1)
+    frames = (g.standard_normal((T, J)) * scale).astype(np.float32)
+    blank = V
+    dw = ol.DecoderWeights(dec)
+    st = {"h": np.zeros((L, P), np.float32), "c": np.zeros((L, P), np.float32), "gp": None}
+
+    def o_predict(k):
+        st["h"], st["c"], st["gp"] = ol.predict(dw, k, st["h"], st["c"])
+
+    def o_joint(t):
+        _, k, di = ol.joint(dw, frames[t], st["gp"])
+        return k, di
+    want = search(T, o_predict, o_joint, blank, durs, 10)
+    dd = hip.DeviceDecoder(dec, torch)
+    try:
+        fd = dev(torch, frames)
+        for call in range(2):
+            say("search in one launch", T, seed, call)
+            got = dd.search(fd, T, blank, durs, 10)
+            assert got == want, (call, len(got), len(want))
+    finally:
+        dd.release()
+    assert len(want) > 0
+
+
+def test_search_bounded_wait_gives_up(hip, torch):
+    """A grid-wide wait whose iteration limit the host sets to 1: the launch
+    ends early (every workgroup leaves at its first wait or on the flag), the
+    call returns PK_HIP_ETIMEOUT, and the next search on the same device
+    with the default limit is whole again."""
+    dec = decoder(23, True)
+    V, J = dec["V"], dec["J"]
+    durs = [0, 1, 2, 3, 4]
+    T = 40
+    frames = (synth.rng(24).standard_normal((T, J)) * 2).astype(np.float32)
+    dd = hip.DeviceDecoder(dec, torch)
+    try:
+        fd = dev(torch, frames)
+        say("search with a wait limit of 1")
+        with pytest.raises(hip.PkHipError) as e:
+            dd.search(fd, T, V, durs, 10, spin_limit=1)
+        assert e.value.code == hip.PK_HIP_ETIMEOUT
+        say("search with the default limit")
+        again = dd.search(fd, T, V, durs, 10)
+        first = dd.search(fd, T, V, durs, 10)
+        assert again == first
+    finally:
+        dd.release()

@@ -119,3 +119,22 @@ def test_device_decoder_is_the_references(hip, tmp_path, seconds, seed, fast):
     finally:
         dd.release()
     assert got == d["toks"] and len(got) > 5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seconds,seed,fast", [(7, 3, 0), (20, 1, 0), (20, 2, 1)])
+def test_device_search_is_the_references(hip, tmp_path, seconds, seed, fast):
+    """The whole search in one launch on the device (pk_hip_search_dev:
+    the LSTM layers, jpred, the joint, its argmax and the duration step
+    with no host round trip) over the reference's joint frames of tiny.pkf:
+    the reference's tokens, frames and durations."""
+    import torch
+    d, _ = reference_decoder(tmp_path, seconds, seed, fast)
+    dd = hip.DeviceDecoder(d["dec"], torch)
+    try:
+        fd = torch.from_numpy(np.ascontiguousarray(d["f"])).cuda()
+        print("[case] device search in one launch", seconds, seed, fast, flush=True)
+        got = dd.search(fd, d["Te"], d["blank"], d["durs"], d["max_symbols"])
+    finally:
+        dd.release()
+    assert got == d["toks"] and len(got) > 5
