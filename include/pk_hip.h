@@ -426,6 +426,13 @@ int pk_hip_force_tiling(int index);
  * bits. */
 int pk_hip_force_split(int splits);
 
+/* Tests and tuning: 0 makes every later search load its LSTM, jpred and
+ * jout panels from memory each token even where they fit resident (gate
+ * panels in registers, the joint's panels in LDS, loaded once a launch:
+ * P and J up to 640, at most 2 LSTM layers), 1 restores that; returns the
+ * previous setting. Both compute the same tokens. */
+int pk_hip_force_search_resident(int on);
+
 /* Tests and tuning: forcing the packed quantize's kernel for every later
  * launch in the process: 0 one wave a column (or a wave a 1024-input chunk
  * of a column over 1024 inputs in blocks), 1 one workgroup a half

@@ -97,6 +97,7 @@ _SIGS = {
     "pk_hip_tilings": (ctypes.c_int, []),
     "pk_hip_force_tiling": (ctypes.c_int, [ctypes.c_int]),
     "pk_hip_force_split": (ctypes.c_int, [ctypes.c_int]),
+    "pk_hip_force_search_resident": (ctypes.c_int, [ctypes.c_int]),
     "pk_hip_gemm_workspace": (ctypes.c_size_t, [ctypes.c_uint32]),
     "pk_hip_tiling_name": (ctypes.c_char_p, [ctypes.c_int]),
     "pk_hip_force_quantize": (ctypes.c_int, [ctypes.c_int]),
@@ -353,6 +354,12 @@ def force_split(splits):
     """Force how many workgroups share a panel in split few-frame products
     (1..8, -1 automatic); returns the one forced before."""
     return lib().pk_hip_force_split(splits)
+
+
+def force_search_resident(on):
+    """Whether later searches keep their panels resident where they fit
+    (the default) or load them each token; returns the previous setting."""
+    return bool(lib().pk_hip_force_search_resident(1 if on else 0))
 
 
 def packed_bytes(n, T):

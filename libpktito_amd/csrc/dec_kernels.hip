@@ -97,6 +97,18 @@ __device__ __forceinline__ int panel_sum(const v4i (&wv)[KU], uint32_t kr, const
     return s;
 }
 
+/* panel_sum over a panel kept in LDS: unit u's bytes at wl + 1 KB u, in
+ * the order panel_load reads them (lane l's 16 bytes at 16 l) */
+template <int KU>
+__device__ __forceinline__ int panel_sum_lds(const int8_t *wl, uint32_t kr, const int8_t *q, int lane) {
+    v4i wv[KU];
+#pragma unroll
+    for (int u = 0; u < KU; u++)
+        if (u < (int)kr)
+            wv[u] = *(const v4i *)(wl + u * kUnitBytes + lane * 16);
+    return panel_sum<KU>(wv, kr, q, lane);
+}
+
 /* Whether a kernel of KU units a panel loads its panels behind its row,
  * before the quantize (one memory round trip instead of two): where the
  * panels fit the registers beside the row (the 64-unit kernels load them
@@ -366,15 +378,57 @@ __device__ __forceinline__ float4 crow4(const float *x, uint32_t i, uint32_t n) 
                        k + 2 < n ? cload(x + k + 2) : 0.0f, k + 3 < n ? cload(x + k + 3) : 0.0f);
 }
 
-template <int CH, int KU>
+template <int CH, int KU, bool RES>
 __global__ __launch_bounds__(256) void search_kernel(SearchArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t q0[64 * KU], q1[64 * KU];
     __shared__ float dq[2], gates[4][16];
     __shared__ uint32_t shared_u[3];
+    /* RES: the jpred panel wg (slot 0) and the jout panels wg and wg + G
+     * (slots 1, 2) of this workgroup, loaded once */
+    __shared__ __attribute__((aligned(16))) int8_t wres[RES ? 3 : 1][RES ? KU * kUnitBytes : 16];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t G = gridDim.x, wg = blockIdx.x;
     const uint32_t P = a.P, J = a.J;
     uint32_t nbar = 0;
+
+    /* RES: each wave's gate panels of every LSTM layer (wx and wh, kResLayers
+     * at most) held in registers for the whole segment, with their rows'
+     * scales and biases; waves 1-3 the scale and bias of their jpred / jout
+     * row */
+    constexpr int RL = RES ? kResLayers : 1, RU = RES ? KU : 1;
+    v4i rwx[RL][RU], rwh[RL][RU];
+    float rxs[RL], rhs[RL], rb[RL], jsr = 0.0f, jbr = 0.0f;
+    if constexpr (RES) {
+        if (wg < P / 16) {
+            const uint32_t j0 = 16 * wg, pn = (wv * P + j0) / 16, r = wv * P + j0 + (lane & 15);
+#pragma unroll
+            for (int l = 0; l < RL; l++)
+                if (l < (int)a.L) {
+                    panel_load<KU>(a.wx[l], a.lstm_stride, pn, a.kr_p, lane, rwx[l]);
+                    panel_load<KU>(a.wh[l], a.lstm_stride, pn, a.kr_p, lane, rwh[l]);
+                    rxs[l] = a.wxs[l][r];
+                    rhs[l] = a.whs[l][r];
+                    rb[l] = a.b[l] ? a.b[l][r] : 0.0f;
+                }
+        }
+        if (wv >= 1) {
+            const bool jp = wv == 1;
+            const uint32_t pn = jp ? wg : wg + (wv - 2) * G, panels = jp ? J / 16 : a.rows_out / 16;
+            if (pn < panels) {
+                const uint32_t kr = jp ? a.kr_p : a.kr_j, r = 16 * pn + (lane & 15);
+                v4i t[KU];
+                panel_load<KU>(jp ? a.jpred : a.jout, jp ? a.jpred_stride : a.jout_stride, pn, kr, lane, t);
+#pragma unroll
+                for (int u = 0; u < KU; u++)
+                    if (u < (int)kr)
+                        *(v4i *)(wres[wv - 1] + u * kUnitBytes + lane * 16) = t[u];
+                const float *bb = jp ? a.jpred_b : a.jout_b;
+                jsr = (jp ? a.jpred_s : a.jout_s)[r];
+                jbr = bb ? bb[r] : 0.0f;
+            }
+        }
+        __syncthreads();
+    }
 
     /* the grid barrier: this workgroup's stores have landed, then it counts
      * itself in and waits for the G arrivals of barrier nbar; false (leave)
@@ -426,11 +480,16 @@ __global__ __launch_bounds__(256) void search_kernel(SearchArgs a) {
         else if (wv == 1)
             load_row<CH>([&](uint32_t i) { return crow4(h_in, i, P); }, P, lane, v);
         const uint32_t pn = (wv * P + j0) / 16;
-        v4i wxv[KU], whv[KU];
-        panel_load<KU>(a.wx[l], a.lstm_stride, pn, a.kr_p, lane, wxv);
-        panel_load<KU>(a.wh[l], a.lstm_stride, pn, a.kr_p, lane, whv);
-        const uint32_t r = wv * P + j0 + (lane & 15);
-        const float wxsr = a.wxs[l][r], whsr = a.whs[l][r], br = a.b[l] ? a.b[l][r] : 0.0f;
+        v4i wxv[RES ? 1 : KU], whv[RES ? 1 : KU];
+        float wxsr = 0.0f, whsr = 0.0f, br = 0.0f;
+        if constexpr (!RES) {
+            panel_load<KU>(a.wx[l], a.lstm_stride, pn, a.kr_p, lane, wxv);
+            panel_load<KU>(a.wh[l], a.lstm_stride, pn, a.kr_p, lane, whv);
+            const uint32_t r = wv * P + j0 + (lane & 15);
+            wxsr = a.wxs[l][r];
+            whsr = a.whs[l][r];
+            br = a.b[l] ? a.b[l][r] : 0.0f;
+        }
         const float cold = threadIdx.x < 16 ? cload(c + j0 + threadIdx.x) : 0.0f;
         if (wv == 0) {
             const float d = quant_loaded<CH>(v, P, a.kr_p, q0, lane);
@@ -442,8 +501,21 @@ __global__ __launch_bounds__(256) void search_kernel(SearchArgs a) {
                 dq[1] = d;
         }
         __syncthreads();
-        const int sx = panel_sum<KU>(wxv, a.kr_p, q0, lane);
-        const int sh = panel_sum<KU>(whv, a.kr_p, q1, lane);
+        int sx = 0, sh = 0;
+        if constexpr (RES) {
+#pragma unroll
+            for (int k = 0; k < RL; k++)
+                if (k == (int)l) {
+                    sx = panel_sum<KU>(rwx[k], a.kr_p, q0, lane);
+                    sh = panel_sum<KU>(rwh[k], a.kr_p, q1, lane);
+                    wxsr = rxs[k];
+                    whsr = rhs[k];
+                    br = rb[k];
+                }
+        } else {
+            sx = panel_sum<KU>(wxv, a.kr_p, q0, lane);
+            sh = panel_sum<KU>(whv, a.kr_p, q1, lane);
+        }
         if (lane < 16) {
             const float g = gemv_out(sx, dq[0], wxsr, a.b[l], br);
             gates[wv][lane] = g + gemv_out(sh, dq[1], whsr, nullptr, 0.0f);
@@ -489,6 +561,28 @@ __global__ __launch_bounds__(256) void search_kernel(SearchArgs a) {
         }
     };
 
+    /* RES: the row quantized by wave 0, then wave w1 sums the panel pn
+     * kept in LDS slot w1 - 1 (jpred: wave 1, panel wg; jout: waves 2 and
+     * 3, panels wg and wg + G) */
+    auto gemv_res = [&](auto value4, uint32_t n, uint32_t kr, const float *bias, uint32_t panels, float *out,
+                        bool joint) {
+        float4 v[CH];
+        if (wv == 0) {
+            load_row<CH>(value4, n, lane, v);
+            const float d = quant_loaded<CH>(v, n, kr, q0, lane);
+            if (lane == 0)
+                dq[0] = d;
+        }
+        __syncthreads();
+        const bool mine = joint ? wv >= 2 : wv == 1;
+        const uint32_t pn = joint ? wg + (wv - 2) * G : wg;
+        if (mine && pn < panels) {
+            const int s = panel_sum_lds<KU>(wres[wv - 1], kr, q0, lane);
+            if (lane < 16)
+                cstore(out + 16 * pn + lane, gemv_out(s, dq[0], jsr, bias, jbr));
+        }
+    };
+
     uint32_t cur = 0;                               /* bit l: which of layer l's two h buffers is current */
     auto predict = [&](uint32_t label) -> bool {
         const float *x = a.embed + (size_t)label * P;
@@ -503,8 +597,11 @@ __global__ __launch_bounds__(256) void search_kernel(SearchArgs a) {
             x = h_out;
         }
         const float *hl = x;
-        gemv([&](uint32_t i) { return crow4(hl, i, P); }, P, a.kr_p, a.jpred, a.jpred_stride, a.jpred_s,
-             a.jpred_b, J / 16, a.gp);
+        if constexpr (RES)
+            gemv_res([&](uint32_t i) { return crow4(hl, i, P); }, P, a.kr_p, a.jpred_b, J / 16, a.gp, false);
+        else
+            gemv([&](uint32_t i) { return crow4(hl, i, P); }, P, a.kr_p, a.jpred, a.jpred_stride, a.jpred_s,
+                 a.jpred_b, J / 16, a.gp);
         return barrier();
     };
 
@@ -512,12 +609,15 @@ __global__ __launch_bounds__(256) void search_kernel(SearchArgs a) {
      * workgroup's wave 0 takes the argmax of all the logits */
     auto joint = [&](uint32_t t, uint32_t &k, uint32_t &di) -> bool {
         const float *ft = a.f + (size_t)t * J;
-        gemv([&](uint32_t i) {
-                 const float4 fv = row4<false>(ft, i, J), gv = crow4(a.gp, i, J);
-                 return make_float4(relu_sum(fv.x, gv.x), relu_sum(fv.y, gv.y), relu_sum(fv.z, gv.z),
-                                    relu_sum(fv.w, gv.w));
-             },
-             J, a.kr_j, a.jout, a.jout_stride, a.jout_s, a.jout_b, a.rows_out / 16, a.logit);
+        auto zrow = [&](uint32_t i) {
+            const float4 fv = row4<false>(ft, i, J), gv = crow4(a.gp, i, J);
+            return make_float4(relu_sum(fv.x, gv.x), relu_sum(fv.y, gv.y), relu_sum(fv.z, gv.z),
+                               relu_sum(fv.w, gv.w));
+        };
+        if constexpr (RES)
+            gemv_res(zrow, J, a.kr_j, a.jout_b, a.rows_out / 16, a.logit, true);
+        else
+            gemv(zrow, J, a.kr_j, a.jout, a.jout_stride, a.jout_s, a.jout_b, a.rows_out / 16, a.logit);
         if (!barrier())
             return false;
         if (wv == 0) {
@@ -644,6 +744,14 @@ int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstr
     return hipPeekAtLastError() == hipSuccess ? 0 : -1;
 }
 
+static bool g_search_resident = true;
+
+bool set_search_resident(bool on) {
+    const bool was = g_search_resident;
+    g_search_resident = on;
+    return was;
+}
+
 size_t search_workspace_bytes(uint32_t L, uint32_t P, uint32_t J, uint32_t rows_out, uint32_t cap) {
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     return up(512) + up((size_t)L * 2 * P * 4) + up((size_t)L * P * 4) + up((size_t)J * 4) + up((size_t)rows_out * 4) +
@@ -677,13 +785,24 @@ int launch_search(SearchArgs &a, void *ws, hipStream_t s) {
         hipMemsetAsync(a.h, 0, up((size_t)a.L * 2 * a.P * 4) + up((size_t)a.L * a.P * 4), s) != hipSuccess ||
         hipMemsetAsync(a.out, 0, 8, s) != hipSuccess)
         return -1;
+    /* resident: every panel's units and every layer's gate panels fit
+     * (kr <= kResUnits, L <= kResLayers), one workgroup a jpred panel and
+     * two a jout panel's pair; else the panels are loaded each token */
+    uint32_t Gr = a.P / 16;
+    Gr = Gr > a.J / 16 ? Gr : a.J / 16;
+    Gr = Gr > (a.rows_out / 16 + 1) / 2 ? Gr : (a.rows_out / 16 + 1) / 2;
+    const bool res = g_search_resident && a.L <= (uint32_t)kResLayers && a.kr_p <= (uint32_t)kResUnits &&
+                     a.kr_j <= (uint32_t)kResUnits && Gr <= 64;
     uint32_t G = a.P / 16;
     G = G > (a.rows_out / 16 + 3) / 4 ? G : (a.rows_out / 16 + 3) / 4;
     G = G > (a.J / 16 + 3) / 4 ? G : (a.J / 16 + 3) / 4;
+    if (res)
+        G = Gr;
     if (G > 64)
         return -2;                              /* the barrier reads every workgroup's slot in one wave */
     void *args[] = { &a };
-    const hipError_t e = hipLaunchCooperativeKernel((const void *)search_kernel<4, 16>, dim3(G), dim3(256), args, 0, s);
+    const void *k = res ? (const void *)search_kernel<4, kResUnits, true> : (const void *)search_kernel<4, 16, false>;
+    const hipError_t e = hipLaunchCooperativeKernel(k, dim3(G), dim3(256), args, 0, s);
     return e == hipSuccess ? 0 : -1;
 }
 

@@ -483,6 +483,8 @@ int pk_hip_force_quantize(int kind) { return pkq8::set_quant_kernel(kind); }
 
 int pk_hip_force_attention(int valu) { return pkq8::set_attention_kernels(valu); }
 
+int pk_hip_force_search_resident(int on) { return pkq8::set_search_resident(on != 0) ? 1 : 0; }
+
 int pk_hip_init(void) {
     std::call_once(g_once, init_once);
     if (g_init != PK_HIP_OK)

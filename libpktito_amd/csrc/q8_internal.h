@@ -172,6 +172,9 @@ int launch_joint(float *logit, uint32_t *tok_dur, const int8_t *w, uint64_t wstr
  * zeroes the arrivals, the flag and the state on s, and launches. 0, -2 for
  * shapes it does not take, -1 for a failed call. */
 constexpr int kMaxDecLayers = 8;
+/* the search keeps its panels resident (gate panels in registers, the
+ * joint's in LDS) up to this many LSTM layers and units a panel row */
+constexpr int kResLayers = 2, kResUnits = 10;
 
 struct SearchArgs {
     const float *f;                                 /* [T][J], the joint's encoder half of each frame */
@@ -194,6 +197,9 @@ struct SearchArgs {
 
 size_t search_workspace_bytes(uint32_t L, uint32_t P, uint32_t J, uint32_t rows_out, uint32_t cap);
 int launch_search(SearchArgs &a, void *ws, hipStream_t s);
+/* tests: false makes the search load its panels each token where they
+ * would fit resident; returns the previous setting */
+bool set_search_resident(bool on);
 
 /* Measurement aids (diag_kernels.hip): an empty launch; a streaming read of
  * bytes (a multiple of 16) at p, 16-byte aligned. */

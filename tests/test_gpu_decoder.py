@@ -217,14 +217,16 @@ def test_greedy_search_on_device(hip, torch):
     assert got == want and len(want) > 3
 
 
+@pytest.mark.parametrize("resident", [True, False])
 @pytest.mark.parametrize("T,seed,scale", [(60, 16, 2.0), (300, 21, 1.0), (5, 22, 3.0)])
-def test_search_in_one_launch(hip, torch, T, seed, scale):
+def test_search_in_one_launch(hip, torch, T, seed, scale, resident):
     """pk_hip_search_dev, the whole search in one cooperative launch, at the
     model's shapes (pred 640, 2 LSTM layers, joint 640, 1024 tokens + blank,
     5 durations): the oracle-driven search's tokens, frames and durations;
     over frames whose scale makes it emit often and others that are mostly
     blank; then the same search again on the same decoder (the state starts
-    from zero each call)."""
+    from zero each call). Both with the panels resident (registers and LDS,
+    loaded once a launch) and loaded each token."""
     dec = decoder(seed, True)
     V, J, L, P = dec["V"], dec["J"], dec["L"], dec["P"]
     durs = [0, 1, 2, 3, 4]
@@ -242,13 +244,15 @@ def test_search_in_one_launch(hip, torch, T, seed, scale):
         return k, di
     want = search(T, o_predict, o_joint, blank, durs, 10)
     dd = hip.DeviceDecoder(dec, torch)
+    was = hip.force_search_resident(resident)
     try:
         fd = dev(torch, frames)
         for call in range(2):
-            say("search in one launch", T, seed, call)
+            say("search in one launch", T, seed, call, "resident" if resident else "loaded")
             got = dd.search(fd, T, blank, durs, 10)
             assert got == want, (call, len(got), len(want))
     finally:
+        hip.force_search_resident(was)
         dd.release()
     assert len(want) > 0
 
