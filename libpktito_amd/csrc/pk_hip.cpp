@@ -15,6 +15,11 @@
 
 #include <algorithm>
 #include <cfenv>
+#include <atomic>
+#include <chrono>
+#include <condition_variable>
+#include <functional>
+#include <thread>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -146,10 +151,11 @@ void free_matrix(pk_hip_q8 *m) {
 /* Host memory that a DMA copy reads or writes must be pinned, and the
  * caller's buffers are not (a mapped model file, malloc'd activations); a
  * copy from pageable memory, and worse a pitched one, runs far below the
- * link's rate. So each context holds two pinned slots: rows are gathered
- * into one on the CPU while the other's DMA runs, and outputs come back the
- * same way in reverse. */
+ * link's rate. So each context holds kSlots pinned slots in a ring: rows are
+ * gathered into one on the CPU while the others' DMAs run, and outputs come
+ * back the same way in reverse. */
 constexpr size_t kSlot = (size_t)4 << 20;
+constexpr int kSlots = 4;
 
 struct Ctx {
     hipStream_t stream = nullptr;
@@ -157,9 +163,9 @@ struct Ctx {
     size_t cap = 0;
     char *skw = nullptr;                    /* the split few-frame products' workspace, zeroed */
     size_t skw_cap = 0;
-    char *host[2] = { nullptr, nullptr };
-    hipEvent_t ev[2] = { nullptr, nullptr };
-    bool used[2] = { false, false };        /* ev[i] was recorded */
+    char *host[kSlots] = {};
+    hipEvent_t ev[kSlots] = {};
+    bool used[kSlots] = {};                 /* ev[i] was recorded */
 };
 
 std::mutex g_ctx_mu;
@@ -187,13 +193,14 @@ int lease(Lease &l) {
     if (!l.c) {
         Ctx *c = new Ctx;
         hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
-        for (int i = 0; i < 2 && e == hipSuccess; i++) {
-            e = hipHostMalloc((void **)&c->host[i], kSlot, hipHostMallocDefault);
-            if (e == hipSuccess)
-                e = hipEventCreateWithFlags(&c->ev[i], hipEventDisableTiming);
-        }
+        /* the first slot now, the others when a call first needs them (a
+         * context that only ever stages small calls holds one) */
+        if (e == hipSuccess)
+            e = hipHostMalloc((void **)&c->host[0], kSlot, hipHostMallocDefault);
+        for (int i = 0; i < kSlots && e == hipSuccess; i++)
+            e = hipEventCreateWithFlags(&c->ev[i], hipEventDisableTiming);
         if (e != hipSuccess) {
-            for (int i = 0; i < 2; i++) {
+            for (int i = 0; i < kSlots; i++) {
                 if (c->ev[i]) (void)hipEventDestroy(c->ev[i]);
                 if (c->host[i]) (void)hipHostFree(c->host[i]);
             }
@@ -206,9 +213,90 @@ int lease(Lease &l) {
     return PK_HIP_OK;
 }
 
+/* Helper threads for the staging copies of large calls: one thread copies a
+ * slot between pinned and pageable memory at ~20-25 GB/s, below the link's
+ * rate, so a slot of a large call is split over the caller and up to
+ * kCopyHelpers more threads. One call uses them at a time; a call that
+ * finds them busy (the reference's pool dealing many small calls at once)
+ * copies alone. The helpers are started on first use, sleep on a condition
+ * variable between calls, and live until the process ends (never joined:
+ * the team is never destroyed). */
+constexpr int kCopyHelpers = 7;
+constexpr size_t kCopySplit = (size_t)1 << 20;    /* copies from this size up are split */
+
+class CopyTeam {
+  public:
+    /* f(part) for part in [0, parts), part 0 on the calling thread;
+     * false (nothing run) when another call holds the team */
+    bool try_run(int parts, const std::function<void(int)> &f) {
+        std::unique_lock<std::mutex> own(run_mu_, std::try_to_lock);
+        if (!own.owns_lock())
+            return false;
+        if (!started_) {
+            for (int i = 0; i < kCopyHelpers; i++)
+                std::thread([this, i] { work(i + 1); }).detach();
+            started_ = true;
+        }
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            fn_ = &f;
+            parts_ = parts;
+            pending_ = parts - 1;
+            gen_++;
+            gen_atomic_.store(gen_, std::memory_order_release);
+        }
+        cv_.notify_all();
+        f(0);
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [this] { return pending_ == 0; });
+        fn_ = nullptr;
+        return true;
+    }
+
+  private:
+    void work(int part) {
+        uint64_t seen = 0;
+        std::unique_lock<std::mutex> lk(mu_);
+        for (;;) {
+            /* a call's next slot comes within tens of microseconds: poll
+             * for it a while before sleeping */
+            if (gen_ == seen) {
+                lk.unlock();
+                const auto t0 = std::chrono::steady_clock::now();
+                while (gen_atomic_.load(std::memory_order_acquire) == seen &&
+                       std::chrono::steady_clock::now() - t0 < std::chrono::microseconds(200))
+                    std::this_thread::yield();
+                lk.lock();
+            }
+            cv_.wait(lk, [&] { return gen_ != seen; });
+            seen = gen_;
+            if (part >= parts_)
+                continue;
+            const std::function<void(int)> *f = fn_;
+            lk.unlock();
+            (*f)(part);
+            lk.lock();
+            if (--pending_ == 0)
+                done_.notify_one();
+        }
+    }
+    std::mutex run_mu_, mu_;
+    std::condition_variable cv_, done_;
+    const std::function<void(int)> *fn_ = nullptr;
+    int parts_ = 0, pending_ = 0;
+    uint64_t gen_ = 0;
+    std::atomic<uint64_t> gen_atomic_{ 0 };
+    bool started_ = false;
+};
+
+CopyTeam &copy_team() {
+    static CopyTeam *t = new CopyTeam;     /* never destroyed: its threads outlive main */
+    return *t;
+}
+
 /* Bytes [b0, b0 + len) of a T x rowbytes block held with a pitch, to or from
  * dense memory: row by row, one memcpy when the pitch is the row. */
-void gather(char *dense, const char *src, size_t b0, size_t len, size_t rowbytes, size_t pitch) {
+void gather_one(char *dense, const char *src, size_t b0, size_t len, size_t rowbytes, size_t pitch) {
     if (pitch == rowbytes) {
         memcpy(dense, src + b0, len);
         return;
@@ -222,7 +310,7 @@ void gather(char *dense, const char *src, size_t b0, size_t len, size_t rowbytes
     }
 }
 
-void scatter(char *dst, const char *dense, size_t b0, size_t len, size_t rowbytes, size_t pitch) {
+void scatter_one(char *dst, const char *dense, size_t b0, size_t len, size_t rowbytes, size_t pitch) {
     if (pitch == rowbytes) {
         memcpy(dst + b0, dense, len);
         return;
@@ -236,7 +324,34 @@ void scatter(char *dst, const char *dense, size_t b0, size_t len, size_t rowbyte
     }
 }
 
+/* the same, a large one split over the copy team (64-byte aligned parts) */
+void split_copy(size_t len, const std::function<void(size_t, size_t)> &part) {
+    if (len >= kCopySplit) {
+        const int parts = kCopyHelpers + 1;
+        const size_t step = ((len + parts - 1) / parts + 63) & ~(size_t)63;
+        const std::function<void(int)> f = [&](int p) {
+            const size_t o = (size_t)p * step;
+            if (o < len)
+                part(o, std::min(step, len - o));
+        };
+        if (copy_team().try_run(parts, f))
+            return;
+    }
+    part(0, len);
+}
+
+void gather(char *dense, const char *src, size_t b0, size_t len, size_t rowbytes, size_t pitch) {
+    split_copy(len, [&](size_t o, size_t n) { gather_one(dense + o, src, b0 + o, n, rowbytes, pitch); });
+}
+
+void scatter(char *dst, const char *dense, size_t b0, size_t len, size_t rowbytes, size_t pitch) {
+    split_copy(len, [&](size_t o, size_t n) { scatter_one(dst, dense + o, b0 + o, n, rowbytes, pitch); });
+}
+
+/* slot i ready for a new copy: allocated, and its last DMA done */
 int slot_free(Ctx *c, int i) {
+    if (!c->host[i])
+        PK_TRY(hipHostMalloc((void **)&c->host[i], kSlot, hipHostMallocDefault));
     if (c->used[i])
         PK_TRY(hipEventSynchronize(c->ev[i]));
     return PK_HIP_OK;
@@ -248,7 +363,7 @@ int h2d(Ctx *c, void *dst, const void *src, size_t rowbytes, size_t nrows, size_
     const size_t total = rowbytes * nrows;
     int e;
     for (size_t b0 = 0, k = 0; b0 < total; b0 += kSlot, k++) {
-        const int i = (int)(k & 1);
+        const int i = (int)(k % kSlots);
         const size_t len = std::min(kSlot, total - b0);
         if ((e = slot_free(c, i)))
             return e;
@@ -266,7 +381,7 @@ int d2h(Ctx *c, void *dst, size_t pitch, const void *src, size_t rowbytes, size_
     const size_t total = rowbytes * nrows, n = (total + kSlot - 1) / kSlot;
     int e;
     auto issue = [&](size_t k) -> int {
-        const int i = (int)(k & 1);
+        const int i = (int)(k % kSlots);
         const size_t b0 = k * kSlot, len = std::min(kSlot, total - b0);
         if ((e = slot_free(c, i)))
             return e;
@@ -275,15 +390,15 @@ int d2h(Ctx *c, void *dst, size_t pitch, const void *src, size_t rowbytes, size_
         c->used[i] = true;
         return PK_HIP_OK;
     };
-    for (size_t k = 0; k < n && k < 2; k++)
+    for (size_t k = 0; k < n && k < (size_t)kSlots; k++)
         if ((e = issue(k)))
             return e;
     for (size_t k = 0; k < n; k++) {
-        const int i = (int)(k & 1);
+        const int i = (int)(k % kSlots);
         const size_t b0 = k * kSlot, len = std::min(kSlot, total - b0);
         PK_TRY(hipEventSynchronize(c->ev[i]));
         scatter((char *)dst, c->host[i], b0, len, rowbytes, pitch);
-        if (k + 2 < n && (e = issue(k + 2)))
+        if (k + kSlots < n && (e = issue(k + kSlots)))
             return e;
     }
     return PK_HIP_OK;
