@@ -233,10 +233,17 @@ class CopyTeam {
         if (!own.owns_lock())
             return false;
         if (!started_) {
-            for (int i = 0; i < kCopyHelpers; i++)
-                std::thread([this, i] { work(i + 1); }).detach();
+            /* a helper that cannot be started leaves the team unusable:
+             * every call then copies alone */
+            try {
+                for (; helpers_ < kCopyHelpers; helpers_++)
+                    std::thread([this, i = helpers_] { work(i + 1); }).detach();
+            } catch (...) {
+            }
             started_ = true;
         }
+        if (helpers_ < kCopyHelpers)
+            return false;
         {
             std::lock_guard<std::mutex> lk(mu_);
             fn_ = &f;
@@ -287,6 +294,7 @@ class CopyTeam {
     uint64_t gen_ = 0;
     std::atomic<uint64_t> gen_atomic_{ 0 };
     bool started_ = false;
+    int helpers_ = 0;
 };
 
 CopyTeam &copy_team() {
