@@ -1,5 +1,6 @@
 /* Test infrastructure: the core/passes.c change a checkout with the hip
- * backend makes, applied at link time to the reference's
+ * backend makes (one pk_k_gemm_q8 and one pk_k_quantize a product when the
+ * hip table is in use), applied at link time to the reference's
  * passes.c compiled unedited where it lies. The link of _ref/dropin_cli_whole
  * renames every call of pk_gemm_on and pk_quantize_on from the library's
  * other files (encoder, decoder, diarizer) to these wrappers
