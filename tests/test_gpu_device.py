@@ -526,3 +526,61 @@ def test_split_deep_products_split_by_themselves(hip, torch, M):
         hip.gemm_q8(host, N, w, ws, None, N, hip.make_act(q, d, K, K, M), 0)
         assert "split" in hip.last_kernel(), hip.last_kernel()
         assert np.array_equal(bits(host), bits(want))
+
+
+STREAM_SHAPES = [(1100, 1024, 2048, 0, 0), (4100, 640, 4096, 1, 1), (2999, 2048, 1040, 1, 4), (777, 4096, 512, 0, 1)]
+
+
+@pytest.mark.parametrize("M,K,N,add,pad", STREAM_SHAPES)
+def test_streamed_tiles_walk_every_tile(hip, torch, M, K, N, add, pad):
+    """Every streamed tiling forced on products whose tiles do not fill the
+    persistent grid evenly (fewer tiles than workgroups, several rounds with
+    a remainder, a partial last channel tile, K = 640 whose units are not a
+    multiple of four), with bias, with and without add, at output strides
+    with and without 16-byte rows (os = N + pad), on packed and row-major
+    activations: every output bit for bit the per-launch pipelined tile's
+    (itself held to the oracle on these shapes' frames sampled here)."""
+    g = synth.rng(M + K + N + pad)
+    w = synth.pack_q8(synth.weights(g, N, K))
+    ws = synth.scales(g, N)
+    bias = g.standard_normal(N).astype(np.float32)
+    x = synth.activations(g, M, K).reshape(-1)
+    q, d = ol.quantize(x, M, K, K, K)
+    os_ = N + pad
+    old = g.standard_normal(M * os_).astype(np.float32)
+    dev = torch.device("cuda")
+    qt = torch.from_numpy(q.reshape(M, K)).to(dev)
+    dt = torch.from_numpy(d).to(dev)
+    bt = torch.from_numpy(bias).to(dev)
+    qp = torch.empty((hip.packed_bytes(K, M),), dtype=torch.int8, device=dev)
+    names = [hip.tiling_name(i) for i in range(hip.tilings())]
+    pipe = names.index("pipe<128x128w8,1,4>")
+    streams = [i for i, n in enumerate(names) if n.startswith("stream")]
+    assert streams
+    outs = {}
+    try:
+        with hip.Q8Matrix(w, ws) as m:
+            xt = torch.from_numpy(x.reshape(M, K)).to(dev)
+            dp = torch.empty((M,), dtype=torch.float32, device=dev)
+            hip.quantize_packed_dev(None, qp, dp, xt, K, M, K)
+            for ti in [pipe] + streams:
+                hip.force_tiling(ti)
+                for packed in (False, True):
+                    say("streamed walk", names[ti], M, K, N, add, pad, "packed" if packed else "rows")
+                    ot = torch.from_numpy(old.reshape(M, os_)).to(dev)
+                    if packed:
+                        hip.gemm_q8_packed_dev(None, os_, m, 0, N, m.dev_scales, bt, qp, dp, K, M, add,
+                                               out_ptr=ot.data_ptr())
+                    else:
+                        hip.gemm_q8_dev(ot, os_, m, 0, N, None, bt, qt, dt, K, K, M, add, ws_ptr=m.dev_scales)
+                    torch.cuda.synchronize()
+                    assert hip.last_kernel() == names[ti], (hip.last_kernel(), names[ti])
+                    outs[(ti, packed)] = ot.cpu().numpy().reshape(M, os_)
+    finally:
+        hip.force_tiling(-1)
+    ref = outs[(pipe, False)]
+    frames = np.unique(np.concatenate([[0, M - 1], synth.rng(M).integers(0, M, 24)]))
+    want = sampled_oracle(q, d, w, ws, bias, K, N, frames, add, old.reshape(M, os_)[:, :N] if add else None)
+    assert np.array_equal(bits(ref[frames, :N]), bits(want))
+    for key, o in outs.items():
+        assert np.array_equal(bits(o), bits(ref)), (names[key[0]], key[1])
