@@ -280,3 +280,42 @@ def test_search_bounded_wait_gives_up(hip, torch):
         assert again == first
     finally:
         dd.release()
+
+
+@pytest.mark.parametrize("P,L,J,V,durs", [(1024, 1, 512, 2000, [0, 1, 2]), (256, 3, 768, 100, [0, 1, 2, 4]),
+                                          (320, 2, 320, 500, [0, 1, 2, 3, 4]), (64, 2, 96, 30, [1, 2])])
+def test_search_in_one_launch_other_shapes(hip, torch, P, L, J, V, durs):
+    """The one-launch search beyond the model's shapes: prediction widths up
+    to 1024 (16 units a panel row, where the panels are loaded each token),
+    one and three LSTM layers, a joint wider than the prediction, a
+    vocabulary of 2000, durations without 0; its tokens, frames and
+    durations the oracle-driven search's, with the panels resident where
+    they fit and loaded each token everywhere."""
+    dec = synth.decoder_weights(synth.rng(P + L + J), P=P, L=L, J=J, V=V, n_dur=len(durs))
+    T = 120
+    frames = (synth.rng(P + J).standard_normal((T, J)) * 2.0).astype(np.float32)
+    blank = V
+    dw = ol.DecoderWeights(dec)
+    st = {"h": np.zeros((L, P), np.float32), "c": np.zeros((L, P), np.float32), "gp": None}
+
+    def o_predict(k):
+        st["h"], st["c"], st["gp"] = ol.predict(dw, k, st["h"], st["c"])
+
+    def o_joint(t):
+        _, k, di = ol.joint(dw, frames[t], st["gp"])
+        return k, di
+    want = search(T, o_predict, o_joint, blank, durs, 10)
+    dd = hip.DeviceDecoder(dec, torch)
+    try:
+        fd = dev(torch, frames)
+        for resident in (True, False):
+            was = hip.force_search_resident(resident)
+            try:
+                say("search in one launch", P, L, J, V, len(durs), "resident" if resident else "loaded")
+                got = dd.search(fd, T, blank, durs, 10)
+            finally:
+                hip.force_search_resident(was)
+            assert got == want, (resident, len(got), len(want))
+    finally:
+        dd.release()
+    assert len(want) > 0
