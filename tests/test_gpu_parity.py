@@ -372,3 +372,42 @@ def test_every_tiling(hip):
                     assert same(out, want), (ti, M, K, N, add)
     finally:
         hip.force_tiling(-1)
+
+
+def test_every_tiling_on_seeded_random_shapes(hip):
+    """30 shapes drawn from a fixed seed (frames 1 to 2600, inputs 32 to
+    4096 including ones that are not a multiple of 64, outputs 16 to 4096
+    including 1040), with bias, add or not, output strides with and without
+    padding (os = 0 at one frame), a run of panels from the middle, under the
+    heuristic and every tiling forced: the oracle's bits."""
+    rng = np.random.default_rng(7)
+    names = [hip.tiling_name(i) for i in range(hip.tilings())]
+    try:
+        for case in range(30):
+            M = int(rng.choice([1, 3, 16, 17, 100, 333, 750, 1201, 2600]))
+            K = int(rng.choice([32, 64, 96, 320, 640, 1024, 1056, 2048, 4096]))
+            N = int(rng.choice([16, 48, 208, 1024, 1040, 2048, 4096]))
+            add = int(rng.integers(0, 2))
+            pad = int(rng.choice([0, 1, 4]))
+            r0 = 16 if N > 32 and rng.integers(0, 2) else 0
+            g = synth.rng(case * 7919 + M + K + N)
+            w = synth.pack_q8(synth.weights(g, N, K))
+            ws = synth.scales(g, N)
+            bias = g.standard_normal(N).astype(np.float32)
+            x = synth.activations(g, M, K).reshape(-1)
+            q, d = ol.quantize(x, M, K, K, K)
+            os_ = 0 if M == 1 else N + pad
+            rows = N - r0
+            base = g.standard_normal(max(1, M * os_ + N)).astype(np.float32)
+            want = base.copy()
+            ol.gemm_q8(want, os_, w, ws, bias, rows, q, d, K, K, M, add, r0=r0, threads=16)
+            with hip.Q8Matrix(w, ws):
+                for ti in [-1] + list(range(hip.tilings())):
+                    hip.force_tiling(ti)
+                    out = base.copy()
+                    say("random shape", case, M, K, N, add, pad, r0, names[ti] if ti >= 0 else "heuristic")
+                    hip.gemm_q8(out, os_, w, ws[r0:], bias[r0:], rows, hip.make_act(q, d, K, K, M), add,
+                                w_offset=r0 * K, out_offset=r0)
+                    assert same(out, want), (case, M, K, N, add, pad, r0, hip.last_kernel())
+    finally:
+        hip.force_tiling(-1)
