@@ -315,21 +315,27 @@ __global__ __launch_bounds__(64 * (WN * WM + NL)) void gemm_stream_kernel(const 
         const Seg &sg = tab.s[j];
         const uint32_t T = sg.T, n0 = tn * BN, m0 = tm * BM, rows = g.rows;
         const float *e = epi[rt & 1];
-        const uint32_t cl = wn * TN * 16 + (lane >> 4) * 4;     /* the lane's first channel in the tile */
-        auto frame = [&](int jj) { return m0 + (wm * TM + jj) * 16 + (lane & 15); };
+        /* the lane index through an empty asm, so that the offsets derived
+         * from it are computed here rather than hoisted and held in
+         * registers across the K loop */
+        uint32_t ln = lane;
+        asm volatile("" : "+v"(ln));
+        const uint32_t cl = wn * TN * 16 + (ln >> 4) * 4;       /* the lane's first channel in the tile */
+        auto frame = [&](int jj) { return m0 + (wm * TM + jj) * 16 + (ln & 15); };
         auto at = [&](int jj, int i) {
             const uint32_t t = frame(jj), c = n0 + cl + i * 16;
             return sg.out + (size_t)(t < T ? t : T - 1) * sg.os + (c < rows ? c : rows - 4);
         };
-        auto value = [&](int jj, int i, float dt) {
-            const float4 wsv = *(const float4 *)&e[BM + cl + i * 16];
+        /* the four outputs of sums s at channel c (tile-local) of one frame */
+        auto value = [&](const v4i &s, uint32_t c, float dt) {
+            const float4 wsv = *(const float4 *)&e[BM + c];
             float4 v;
-            v.x = __builtin_fmaf((float)acc[i][jj][0], dt, 0.0f) * wsv.x;
-            v.y = __builtin_fmaf((float)acc[i][jj][1], dt, 0.0f) * wsv.y;
-            v.z = __builtin_fmaf((float)acc[i][jj][2], dt, 0.0f) * wsv.z;
-            v.w = __builtin_fmaf((float)acc[i][jj][3], dt, 0.0f) * wsv.w;
+            v.x = __builtin_fmaf((float)s[0], dt, 0.0f) * wsv.x;
+            v.y = __builtin_fmaf((float)s[1], dt, 0.0f) * wsv.y;
+            v.z = __builtin_fmaf((float)s[2], dt, 0.0f) * wsv.z;
+            v.w = __builtin_fmaf((float)s[3], dt, 0.0f) * wsv.w;
             if (g.bias) {
-                const float4 bv = *(const float4 *)&e[BM + BN + cl + i * 16];
+                const float4 bv = *(const float4 *)&e[BM + BN + c];
                 v.x = v.x + bv.x;
                 v.y = v.y + bv.y;
                 v.z = v.z + bv.z;
@@ -337,48 +343,91 @@ __global__ __launch_bounds__(64 * (WN * WM + NL)) void gemm_stream_kernel(const 
             }
             return v;
         };
+        /* The vector stores write whole 128-byte lines, each from 8
+         * consecutive lanes in address order, where a block's own layout
+         * stores 64 bytes of 16 frames, one frame a lane (measured: ff up at
+         * ten minutes of audio 52.1-52.6 -> 49.6-50.4 us; the same store
+         * pattern without the moves below 45.7-46.9 us, which is what they
+         * cost). The sums move as integers before the epilogue, so
+         * the bits are the same: channel blocks 2k and 2k + 1 pair up and
+         * swap the block for the lane's bit 3 (lanes l and l ^ 8 exchange
+         * through DPP row_ror:8, a rotation by 8 inside each row of 16
+         * lanes), so that each register of a pair holds 8 frames x 32
+         * channels, lane (r, b, f) channel 16 b + 4 r of frame f; then one
+         * ds_bpermute a dword moves it to lane 8 f + 4 b + r, whose 16 bytes
+         * are chunk 4 b + r of frame f's line. */
+        static_assert(TN % 2 == 0, "channel blocks pair up");
+        constexpr int NP = TN / 2;
+        const uint32_t hi = (ln >> 3) & 1;
+        /* the lane this one takes its sums from after the swap, in bytes */
+        const int src = (int)((((ln & 3) << 4) | (((ln >> 2) & 1) << 3) | (ln >> 3)) * 4);
+        const uint32_t cp = wn * TN * 16 + (ln & 7) * 4;                 /* the lane's first channel in pair 0 */
+        auto frame2 = [&](int jj, int h) { return m0 + (wm * TM + jj) * 16 + h * 8 + (ln >> 3); };
+        auto at2 = [&](int jj, int k, int h) {
+            const uint32_t t = frame2(jj, h), c = n0 + cp + k * 32;
+            return sg.out + (size_t)(t < T ? t : T - 1) * sg.os + (c < rows ? c : rows - 4);
+        };
         /* one straight-line epilogue each for plain and residual-adding
-         * vector stores (with add, frame row jj + 1's residuals load before
-         * row jj's stores issue, so a row's wait, vmcnt counting stores too,
-         * waits for the stores of two rows back, never the last row's) */
+         * vector stores (with add, frame block jj + 1's residuals load before
+         * block jj's stores issue, so a block's wait, vmcnt counting stores
+         * too, waits for the stores of two blocks back, never the last one's) */
         auto vec_rows = [&](auto addc) {
             constexpr bool ADD = decltype(addc)::value;
             float4 old[2][TN];
-            if constexpr (ADD) {
+            auto load_old = [&](int jj, float4 *o) {
 #pragma unroll
-                for (int i = 0; i < TN; i++)
-                    old[0][i] = *(const float4 *)at(0, i);
-            }
+                for (int k = 0; k < NP; k++)
+#pragma unroll
+                    for (int h = 0; h < 2; h++)
+                        o[k * 2 + h] = *(const float4 *)at2(jj, k, h);
+            };
+            if constexpr (ADD)
+                load_old(0, old[0]);
 #pragma unroll
             for (int jj = 0; jj < TM; jj++) {
                 if constexpr (ADD) {
-                    if (jj + 1 < TM) {
+                    if (jj + 1 < TM)
+                        load_old(jj + 1, old[(jj + 1) & 1]);
+                }
+                float dt[2];
 #pragma unroll
-                        for (int i = 0; i < TN; i++)
-                            old[(jj + 1) & 1][i] = *(const float4 *)at(jj + 1, i);
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t t = frame2(jj, h);
+                    dt[h] = e[(t < T ? t : T - 1) - m0];
+                }
+#pragma unroll
+                for (int k = 0; k < NP; k++) {
+                    v4i x[2];
+#pragma unroll
+                    for (int d = 0; d < 4; d++) {
+                        const int a = acc[2 * k][jj][d], bq = acc[2 * k + 1][jj][d];
+                        const int ar = __builtin_amdgcn_update_dpp(0, a, 0x128, 0xF, 0xF, false);
+                        const int br = __builtin_amdgcn_update_dpp(0, bq, 0x128, 0xF, 0xF, false);
+                        x[0][d] = __builtin_amdgcn_ds_bpermute(src, hi ? br : a);     /* frames 0-7 of the block */
+                        x[1][d] = __builtin_amdgcn_ds_bpermute(src, hi ? bq : ar);    /* frames 8-15 */
+                    }
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const uint32_t t = frame2(jj, h);
+                        float4 v = value(x[h], cp + k * 32, dt[h]);
+                        if constexpr (ADD) {
+                            const float4 o4 = old[jj & 1][k * 2 + h];
+                            v.x = o4.x + v.x;
+                            v.y = o4.y + v.y;
+                            v.z = o4.z + v.z;
+                            v.w = o4.w + v.w;
+                            /* the sums happen on every lane, so every residual
+                             * load is waited for here and none is left in
+                             * flight into the next tile's loop (whose register
+                             * writes would then wait on vmcnt, stores
+                             * included) */
+                            asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+                        }
+                        if (t < T && n0 + cp + k * 32 < rows)
+                            store_out4(at2(jj, k, h), v, g.plain);
                     }
                 }
-                const uint32_t t = frame(jj);
-                const float dt = e[(t < T ? t : T - 1) - m0];
-#pragma unroll
-                for (int i = 0; i < TN; i++) {
-                    float4 v = value(jj, i, dt);
-                    if constexpr (ADD) {
-                        const float4 o4 = old[jj & 1][i];
-                        v.x = o4.x + v.x;
-                        v.y = o4.y + v.y;
-                        v.z = o4.z + v.z;
-                        v.w = o4.w + v.w;
-                        /* the sums happen on every lane, so every residual
-                         * load is waited for here and none is left in flight
-                         * into the next tile's loop (whose register writes
-                         * would then wait on vmcnt, stores included) */
-                        asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
-                    }
-                    if (t < T && n0 + cl + i * 16 < rows)
-                        store_out4(at(jj, i), v, g.plain);
-                }
-                __builtin_amdgcn_sched_barrier(0);      /* one frame row's registers at a time */
+                __builtin_amdgcn_sched_barrier(0);      /* one frame block's registers at a time */
             }
         };
         if (((sg.os & 3) == 0) && ((((uintptr_t)sg.out) & 15) == 0)) {
@@ -393,7 +442,7 @@ __global__ __launch_bounds__(64 * (WN * WM + NL)) void gemm_stream_kernel(const 
                 const float dt = e[(t < T ? t : T - 1) - m0];
 #pragma unroll
                 for (int i = 0; i < TN; i++) {
-                    const float4 v = value(jj, i, dt);
+                    const float4 v = value(acc[i][jj], cl + i * 16, dt);
                     if (t < T && n0 + cl + i * 16 < rows) {
                         float *o = at(jj, i);
                         store_out1(o, g.add ? o[0] + v.x : v.x, g.plain);
