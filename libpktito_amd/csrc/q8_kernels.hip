@@ -1978,19 +1978,28 @@ static bool stream_spans_fit(const GemmArgs &g, const Seg &sg) {
  * with deep inputs (4096). Measured at 7500 frames (each product alone): ff
  * up 41-44 against 46-47 us, pw1 24.2 against 25.9, the positions' 14999
  * rows 26-30 against 28-34, ff down 32.7-34.3 against 34.2-36.1; the 236-tile
- * products with 1024 inputs (q, k, v, o, pw2) and the attention's batch run
- * faster on the per-launch tiles (two workgroups a CU fill each other's
- * barrier waits where one tile a CU leaves nothing to stream). */
+ * products with 1024 inputs (q, k, v, o, pw2) run faster on the per-launch
+ * tiles (two workgroups a CU fill each other's barrier waits where one tile
+ * a CU leaves nothing to stream: q 15.3 against 16.5 us, o 18.6 against
+ * 19.6). A batch (its rows the largest job's, its frames all jobs') takes
+ * 128 x 256 streamed tiles where there are at least 1024 of them: the
+ * attention's q, k, v and positions at 7500 frames 58.2-58.7 us against
+ * 64.8-65.7 on the per-launch tiles (61.1-61.4 on 256 x 128) with the batch
+ * alone, 63.2 against 64.8 inside the 24-layer sweep (each layer's weights
+ * cold). */
 static int pick_stream(uint32_t rows, uint64_t frames, uint32_t ku, bool batch = false) {
     if (g_forced_ring >= kNRing) {
         const int i = g_forced_ring - kNRing;
         return stream_fits(i, ku) ? i : -1;
     }
-    if (g_forced_ring >= 0 || batch || !stream_fits(0, ku))
+    const int i = batch ? 1 : 0;
+    if (g_forced_ring >= 0 || !stream_fits(i, ku))
         return -1;
-    const StreamCfg &c = *stream_cfg(0);
+    const StreamCfg &c = *stream_cfg(i);
     const uint64_t tiles = (uint64_t)((rows + c.bn - 1) / c.bn) * ((frames + c.bm - 1) / c.bm);
-    return tiles >= 400 || (ku >= 64 && tiles >= 200) ? 0 : -1;
+    if (batch)
+        return tiles >= 1024 ? i : -1;
+    return tiles >= 400 || (ku >= 64 && tiles >= 200) ? i : -1;
 }
 
 template <int WN, int WM, int TN, int TM, int MODE>
