@@ -15,9 +15,12 @@
  *     epilogue buffers. They alone wait on vmcnt.
  *   - WN x WM MFMA waves read fragments from the ring (two register sets, the
  *     next sub-step's reads issued before this one's MFMAs), multiply, and at
- *     a tile's end run the epilogue from registers and store the outputs.
- *     They never wait on vmcnt (the counter also counts stores on gfx950), so
- *     a tile's stores drain while the next tile's K loop runs.
+ *     a tile's end move their sums across lanes so that consecutive lanes hold
+ *     consecutive bytes of each output line, run the epilogue from registers
+ *     and store the outputs. They never wait on vmcnt in the K loop (the
+ *     counter also counts stores on gfx950), so a tile's stores drain while
+ *     the next tile's K loop runs; only a residual-adding epilogue waits, for
+ *     its residuals.
  *
  * One s_barrier a stage meets both: the loaders arrive once the next stage has
  * landed, the MFMA waves once they hold the current stage's last fragments in
