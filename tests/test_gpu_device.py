@@ -85,7 +85,10 @@ def test_layer_products_ten_minutes(hip, torch, prod):
 @pytest.mark.parametrize("K,N", [(1024, 4096), (4096, 1024)])
 def test_ragged_batch_grouped(hip, torch, K, N):
     """Eight segments of 150-750 frames (12-60 s) in one launch: each
-    segment's outputs are the bits of its own product, and the oracle's."""
+    segment's outputs are the bits of its own product, and the oracle's; and
+    the same grouped launch under every tiling forced (the 128 x 128 and
+    larger tiles store whole lines from consecutive lanes across segment
+    ends)."""
     lens = synth.ragged_lengths()
     g = synth.rng(K + N)
     w = synth.pack_q8(synth.weights(g, N, K))
@@ -108,12 +111,26 @@ def test_ragged_batch_grouped(hip, torch, K, N):
         for o2, qt, dt, L in solo:
             hip.gemm_q8_dev(o2, N, m, 0, N, None, None, qt, dt, K, K, L, 0, ws_ptr=m.dev_scales)
         torch.cuda.synchronize()
-    for (ot, _, _, _, _, _, L), (o2, _, _, _), (q, d, _) in zip(segs, solo, host):
-        a, b = ot.cpu().numpy(), o2.cpu().numpy()
-        assert np.array_equal(bits(a), bits(b))
-        frames = np.unique(np.concatenate([[0, L - 1], synth.rng(L).integers(0, L, 24)]))
-        want = sampled_oracle(q, d, w, ws, None, K, N, frames)
-        assert np.array_equal(bits(a[frames]), bits(want))
+        for (ot, _, _, _, _, _, L), (o2, _, _, _), (q, d, _) in zip(segs, solo, host):
+            a, b = ot.cpu().numpy(), o2.cpu().numpy()
+            assert np.array_equal(bits(a), bits(b))
+            frames = np.unique(np.concatenate([[0, L - 1], synth.rng(L).integers(0, L, 24)]))
+            want = sampled_oracle(q, d, w, ws, None, K, N, frames)
+            assert np.array_equal(bits(a[frames]), bits(want))
+        # the grouped launch under every tiling forced (each segment's own
+        # launch above, checked against the oracle, is the reference)
+        try:
+            for ti in range(hip.tilings()):
+                hip.force_tiling(ti)
+                for (ot, *_rest) in segs:
+                    ot.fill_(7.0)
+                say("grouped forced", ti, K, N)
+                hip.gemm_q8_grouped_dev(m, 0, N, m.dev_scales, None, segs, 0)
+                torch.cuda.synchronize()
+                for j, ((ot, *_r1), (o2, *_r2)) in enumerate(zip(segs, solo)):
+                    assert torch.equal(ot.view(torch.int32), o2.view(torch.int32)), (ti, j, hip.last_kernel())
+        finally:
+            hip.force_tiling(-1)
 
 
 def test_interior_panels_device(hip, torch):
